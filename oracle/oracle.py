@@ -1,0 +1,316 @@
+"""CPU oracle for the paged-attention path — TEST INFRASTRUCTURE ONLY.
+
+Python side of the plain-C restatement in ``oracle.c`` (loaded through ctypes)
+plus the two pieces of reference host logic the checks need: the tiling policy
+that decides which reference numerics a row gets, and the reference's error
+gate. Only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
+``bench.py`` may import this module, and only as the checker.
+
+Parity status (how each oracle function is pinned; see tests/test_oracle.py):
+
+- ``bf16_from_f32``: torch's CPU ``.to(torch.bfloat16)`` (an independent RNE
+  implementation) on random, tie, NaN and overflow inputs.
+- ``bf16_from_f64``: the known answer of tests/decoder_cpu_reference_test.py:66-68
+  (1 + 2^-8 + 2^-32 -> 1 + 2^-7), exact rational rounding with ``fractions`` on
+  random normals, subnormals and ties, the overflow boundary, and rejection of
+  non-finite input.
+- ``kv_store``: brute-force per-slot audit (every targeted slot holds its row,
+  every other byte keeps its sentinel, rows >= valid_rows are never written),
+  as in tests/fixed_kv_descriptor_device_test.cpp:146-197.
+- ``tile_indices``: the expected index table of tests/attention_plan_smoke.py:32-40.
+- ``direct_bf16_pv`` / ``tiled_bf16_pv`` / ``direct_tiled``: the invariant of
+  tests/paged_attention_reference_test.py:48-50 on the reference test's own
+  seeded inputs (torch.manual_seed(771)), closed forms (one key -> the value row;
+  equal scores -> the mean), the fp64 gate, and single-tile reduction
+  (tiled with one tile == direct up to one bf16 ulp).
+- ``fp64_attention``: closed forms and a brute-force numpy float64 softmax.
+- ``guid_attention``: closed forms, the fp64 gate, and the single-tile path
+  agreeing with direct_bf16_pv.
+- ``isolated_errors``: the known answers of
+  tests/paged_attention_reference_test.py:52-59.
+"""
+
+import ctypes
+import os
+import pathlib
+
+import numpy as np
+
+_HERE = pathlib.Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle.so"
+
+
+def build():
+    """Compile liboracle.so with the committed Makefile."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+
+
+def _load():
+    if not _LIB_PATH.exists():
+        build()
+    lib = ctypes.CDLL(str(_LIB_PATH))
+    lib.orc_bf16_from_f32.restype = ctypes.c_uint16
+    lib.orc_bf16_from_f32.argtypes = [ctypes.c_float]
+    lib.orc_bf16_to_f32.restype = ctypes.c_float
+    lib.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+def _ptr(array, ctype):
+    return array.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+class AttentionArgs(ctypes.Structure):
+    _fields_ = [
+        ("query", ctypes.c_void_p), ("q_stride", ctypes.c_int64),
+        ("key_pool", ctypes.c_void_p), ("value_pool", ctypes.c_void_p),
+        ("slot_stride", ctypes.c_int64), ("head_stride", ctypes.c_int64),
+        ("requests", ctypes.c_void_p), ("positions", ctypes.c_void_p),
+        ("mapping", ctypes.c_void_p), ("context", ctypes.c_int64), ("rows", ctypes.c_int64),
+        ("heads", ctypes.c_int32), ("kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("softcap", ctypes.c_float), ("sliding_window", ctypes.c_int32),
+        ("threads", ctypes.c_int32),
+    ]
+
+
+# ---------------------------------------------------------------------------
+# Scalar conversions
+# ---------------------------------------------------------------------------
+
+def bf16_from_f32(values):
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(values.shape, dtype=np.uint16)
+    lib().orc_bf16_from_f32_array(_ptr(values, ctypes.c_float), _ptr(out, ctypes.c_uint16),
+                                  ctypes.c_int64(values.size))
+    return out
+
+
+def bf16_to_f32(bits):
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_from_f64(values):
+    """Direct binary64 -> bf16 RNE (tests/fp64_reference.py:7-29). Raises on non-finite input."""
+    values = np.ascontiguousarray(values, dtype=np.float64)
+    out = np.empty(values.shape, dtype=np.uint16)
+    status = lib().orc_bf16_from_f64_array(_ptr(values, ctypes.c_double), _ptr(out, ctypes.c_uint16),
+                                           ctypes.c_int64(values.size))
+    if status != 0:
+        raise ValueError("nonfinite FP64 reference")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# KV store and indexing
+# ---------------------------------------------------------------------------
+
+def kv_store(key, value, locations, valid_rows, pool, slots, kv_heads, head_dim):
+    """Head-major KV store into ``pool`` (uint16 [2, Hkv, S, d] or flat), in place.
+
+    ``key``/``value`` are uint16 [rows, Hkv * d] (row stride may exceed the width).
+    """
+    assert key.dtype == np.uint16 and value.dtype == np.uint16 and pool.dtype == np.uint16
+    assert key.strides == value.strides and key.strides[1] == 2
+    assert pool.flags["C_CONTIGUOUS"]
+    locations = np.ascontiguousarray(locations, dtype=np.int32)
+    row_stride = key.strides[0] // 2
+    lib().orc_kv_store(ctypes.c_void_p(key.ctypes.data), ctypes.c_void_p(value.ctypes.data),
+                       ctypes.c_int64(row_stride), _ptr(locations, ctypes.c_int32),
+                       ctypes.c_int32(valid_rows), _ptr(pool, ctypes.c_uint16),
+                       ctypes.c_int64(slots), ctypes.c_int32(kv_heads), ctypes.c_int32(head_dim))
+    return pool
+
+
+def tile_indices(mapping, requests, work, context):
+    mapping = np.ascontiguousarray(mapping, dtype=np.int32)
+    requests = np.ascontiguousarray(requests, dtype=np.int32)
+    work = np.ascontiguousarray(work, dtype=np.int32).reshape(-1, 4)
+    out = np.empty((work.shape[0], 64), dtype=np.int32)
+    lib().orc_tile_indices(_ptr(mapping, ctypes.c_int32), _ptr(requests, ctypes.c_int32),
+                           _ptr(work, ctypes.c_int32), ctypes.c_int64(work.shape[0]),
+                           ctypes.c_int32(context), _ptr(out, ctypes.c_int32))
+    return out
+
+
+def mapping_from_block_table(block_table, block_size, context):
+    block_table = np.ascontiguousarray(block_table, dtype=np.int32)
+    requests, max_blocks = block_table.shape
+    mapping = np.empty((requests, context), dtype=np.int32)
+    lib().orc_mapping_from_block_table(_ptr(block_table, ctypes.c_int32), ctypes.c_int64(requests),
+                                       ctypes.c_int64(max_blocks), ctypes.c_int32(block_size),
+                                       ctypes.c_int64(context), _ptr(mapping, ctypes.c_int32))
+    return mapping
+
+
+# ---------------------------------------------------------------------------
+# Attention references
+# ---------------------------------------------------------------------------
+
+class Problem:
+    """One paged-attention problem in the reference's row form.
+
+    query: uint16 [rows, heads * d]; pool: uint16 head-major [2, Hkv, S, d];
+    requests/positions: int64 [rows]; mapping: int32 [requests, context].
+    """
+
+    def __init__(self, query, pool, requests, positions, mapping, heads, kv_heads, head_dim, scale,
+                 softcap=0.0, sliding_window=-1):
+        self.query = np.ascontiguousarray(query, dtype=np.uint16)
+        self.pool = np.ascontiguousarray(pool, dtype=np.uint16)
+        self.requests = np.ascontiguousarray(requests, dtype=np.int64)
+        self.positions = np.ascontiguousarray(positions, dtype=np.int64)
+        self.mapping = np.ascontiguousarray(mapping, dtype=np.int32)
+        self.heads, self.kv_heads, self.head_dim = int(heads), int(kv_heads), int(head_dim)
+        self.scale = float(np.float32(scale))
+        self.softcap = float(softcap)
+        self.sliding_window = int(sliding_window)
+        self.slots = self.pool.size // (2 * self.kv_heads * self.head_dim)
+        assert self.query.shape[1] >= self.heads * self.head_dim
+
+    def args(self, threads):
+        half = self.kv_heads * self.slots * self.head_dim
+        base = self.pool.ctypes.data
+        return AttentionArgs(
+            self.query.ctypes.data, self.query.shape[1], base, base + 2 * half,
+            self.head_dim, self.slots * self.head_dim,
+            self.requests.ctypes.data, self.positions.ctypes.data, self.mapping.ctypes.data,
+            self.mapping.shape[1], self.query.shape[0], self.heads, self.kv_heads, self.head_dim,
+            self.scale, self.softcap, self.sliding_window, threads)
+
+    def _out16(self):
+        return np.zeros((self.query.shape[0], self.heads * self.head_dim), dtype=np.uint16)
+
+
+def _threads(threads):
+    if threads is None:
+        return max(1, min(16, os.cpu_count() or 1))
+    return threads
+
+
+def _check(status):
+    if status != 0:
+        raise RuntimeError(f"oracle attention failed with status {status}")
+
+
+def direct_bf16_pv(p, threads=None):
+    out = p._out16()
+    args = p.args(_threads(threads))
+    _check(lib().orc_direct_bf16_pv(ctypes.byref(args), _ptr(out, ctypes.c_uint16)))
+    return out
+
+
+def tiled_bf16_pv(p, kv_tile, threads=None):
+    out = p._out16()
+    args = p.args(_threads(threads))
+    _check(lib().orc_tiled_bf16_pv(ctypes.byref(args), ctypes.c_int32(kv_tile), _ptr(out, ctypes.c_uint16)))
+    return out
+
+
+def direct_tiled(p, kv_tile, threads=None):
+    out = p._out16()
+    args = p.args(_threads(threads))
+    _check(lib().orc_direct_tiled(ctypes.byref(args), ctypes.c_int32(kv_tile), _ptr(out, ctypes.c_uint16)))
+    return out
+
+
+def fp64_attention(p, threads=None):
+    out = np.zeros((p.query.shape[0], p.heads * p.head_dim), dtype=np.float64)
+    args = p.args(_threads(threads))
+    _check(lib().orc_fp64_attention(ctypes.byref(args), _ptr(out, ctypes.c_double)))
+    return out
+
+
+def fp64_bf16(p, threads=None):
+    """fp64 attention rounded once to bf16 (the reference's ``direct_bf16``), as float64."""
+    return bf16_to_f32(bf16_from_f64(fp64_attention(p, threads))).astype(np.float64)
+
+
+def fp32_softmax_attention(p, threads=None):
+    out = p._out16()
+    args = p.args(_threads(threads))
+    _check(lib().orc_fp32_softmax_attention(ctypes.byref(args), _ptr(out, ctypes.c_uint16)))
+    return out
+
+
+def guid_attention(p, tiles_per_row, kv_tile=512, threads=None):
+    out = p._out16()
+    tiles = np.ascontiguousarray(tiles_per_row, dtype=np.int32)
+    args = p.args(_threads(threads))
+    _check(lib().orc_guid_attention(ctypes.byref(args), _ptr(tiles, ctypes.c_int32), ctypes.c_int32(kv_tile),
+                                    _ptr(out, ctypes.c_uint16)))
+    return out
+
+
+def reference_tiles_per_row(sequences, query_heads, kv_heads, head_dim, total_rows):
+    """Number of 512-key tiles the reference runs for each row's query block.
+
+    Restates the tiling policy of src/bridge/attention_plan.cpp:184-262 without
+    a sliding window: ``sequences`` is a list of (first_row, length, prefix).
+    A value of 1 means the single fused (direct softmax) launch.
+    """
+    out = np.zeros(total_rows, dtype=np.int32)
+    for first_row, length, prefix in sequences:
+        done = 0
+        while done < length:
+            remaining = length - done
+            full_visible = prefix + done + remaining
+            decode = remaining == 1
+            end = full_visible
+            count = min(remaining, 256)
+            q_bucket = 1 << (count - 1).bit_length()
+            if decode and 512 < end <= 8192:
+                direct_kv = (end + 511) & ~511
+            else:
+                direct_kv = max(128, 1 << (end - 1).bit_length())
+            fused_bytes = direct_kv * (4 * kv_heads * head_dim + 10 * query_heads)
+            single_decode = decode and (end <= 4096 or (end <= 8192 and fused_bytes <= 40 * 1024 * 1024))
+            short_prefill = end <= 512 and q_bucket * direct_kv * query_heads <= 4 * 1024 * 1024
+            if not single_decode and not short_prefill:
+                row_cap = 512 if length >= 2048 else 256
+                max_rows = min(row_cap, (16 * 1024 * 1024) // (512 * query_heads))
+                max_rows = 1 << (max_rows.bit_length() - 1)
+                count = min(remaining, max_rows)
+            visible = prefix + done + count
+            kv_bucket = direct_kv if (single_decode or short_prefill) else 512
+            tiles = (visible + kv_bucket - 1) // kv_bucket
+            out[first_row + done:first_row + done + count] = tiles
+            done += count
+    return out
+
+
+def isolated_errors(actual, fp64, tiled, tiled_gate=5e-3):
+    """Relative-L2 gate of tests/paged_attention_reference.py:60-69 (numpy restatement).
+
+    ``tiled_gate`` is 5e-3 in that file; the reference's device tests use 1e-3
+    (tests/fused_paged_decode_device_test.cpp:458).
+    """
+    actual, fp64, tiled = (np.asarray(v, dtype=np.float64) for v in (actual, fp64, tiled))
+    assert actual.shape == fp64.shape == tiled.shape and actual.ndim >= 2
+    assert all(np.isfinite(v).all() for v in (actual, fp64, tiled))
+    actual, fp64, tiled = (v.reshape(v.shape[0], -1) for v in (actual, fp64, tiled))
+    error64 = (np.linalg.norm(actual - fp64, axis=-1) /
+               np.maximum(np.linalg.norm(fp64, axis=-1), 1e-30)).max()
+    error_tiled = (np.linalg.norm(actual - tiled, axis=-1) /
+                   np.maximum(np.linalg.norm(tiled, axis=-1), 1e-30)).max()
+    assert error64 <= 1e-2 and error_tiled <= tiled_gate, (error64, error_tiled)
+    return float(error64), float(error_tiled)
+
+
+def tolerance_errors(actual_bits, reference_bits):
+    """(max_abs, mean_abs) between two bf16 bit arrays, compared as float64."""
+    a = bf16_to_f32(actual_bits).astype(np.float64)
+    b = bf16_to_f32(reference_bits).astype(np.float64)
+    diff = np.abs(a - b)
+    return float(diff.max()), float(diff.mean())
