@@ -1,0 +1,128 @@
+"""ctypes binding of the C ABI in include/gaudirt_amd.h.
+
+This is the thin Python view of ``libgaudirt_amd.so`` that the GPU tests and the
+benchmark call through: device buffers are torch tensors on ``cuda``, passed by
+pointer together with the current HIP stream. Loading fails loudly when the
+library has not been built; there is no other implementation behind it.
+"""
+
+import ctypes
+import pathlib
+
+PACKAGE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = PACKAGE / "libgaudirt_amd.so"
+
+GK_OK = 0
+GK_ERR_INVALID_ARGUMENT = 1
+GK_ERR_UNSUPPORTED = 2
+GK_ERR_HIP = 3
+GK_ERR_OUT_OF_MEMORY = 4
+GK_ERR_WORKSPACE = 5
+
+# Every function include/gaudirt_amd.h declares (checked by tests/test_capi.py).
+EXPORTED = [
+    "gk_last_error", "gk_version", "gk_kv_store", "gk_paged_decode_workspace_bytes",
+    "gk_paged_decode_partition_tokens", "gk_paged_decode", "gk_split_k_merge", "gk_paged_prefill",
+    "gk_paged_prefill_workspace_bytes", "gk_attn_tile_indices", "gk_advance_decode_lengths",
+    "gk_allocator_create", "gk_allocator_destroy", "gk_allocator_alloc", "gk_allocator_record_stream",
+    "gk_allocator_free", "gk_allocator_empty_cache", "gk_allocator_get_stats",
+]
+
+c_void_p = ctypes.c_void_p
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_f32 = ctypes.c_float
+
+
+class DecodeParams(ctypes.Structure):
+    _fields_ = [
+        ("query", c_void_p), ("q_row_stride", c_i64),
+        ("pool", c_void_p), ("slots", c_i64),
+        ("block_tables", c_void_p), ("bt_stride", c_i64), ("block_size", c_i32),
+        ("row_request", c_void_p), ("row_context", c_void_p), ("rows", c_i32),
+        ("q_heads", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32),
+        ("scale", c_f32), ("softcap", c_f32), ("sliding_window", c_i32),
+        ("max_context", c_i32), ("partition_tokens", c_i32),
+        ("out", c_void_p), ("out_row_stride", c_i64),
+        ("new_key", c_void_p), ("new_value", c_void_p), ("new_kv_row_stride", c_i64),
+        ("slot_mapping", c_void_p),
+    ]
+
+
+class PrefillParams(ctypes.Structure):
+    _fields_ = [
+        ("query", c_void_p), ("q_row_stride", c_i64),
+        ("pool", c_void_p), ("slots", c_i64),
+        ("block_tables", c_void_p), ("bt_stride", c_i64), ("block_size", c_i32),
+        ("seq_request", c_void_p), ("seq_prefix", c_void_p), ("seq_rows", c_void_p),
+        ("seq_first_row", c_void_p), ("seqs", c_i32), ("max_rows", c_i32),
+        ("q_heads", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32),
+        ("scale", c_f32), ("softcap", c_f32), ("sliding_window", c_i32),
+        ("out", c_void_p), ("out_row_stride", c_i64),
+    ]
+
+
+class AllocatorStats(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_uint64) for name in (
+        "allocated_bytes", "peak_bytes", "reserved_bytes", "largest_free_block", "slabs", "events_created")]
+
+
+class GkError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__(f"gaudirt_amd error {code}: {message}")
+        self.code = code
+
+
+_lib = None
+
+
+def load():
+    """Load libgaudirt_amd.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: run `python -m gaudirt_amd.build` first")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    lib.gk_last_error.restype = ctypes.c_char_p
+    lib.gk_version.restype = ctypes.c_char_p
+    lib.gk_paged_decode_workspace_bytes.restype = ctypes.c_size_t
+    lib.gk_paged_decode_workspace_bytes.argtypes = [ctypes.POINTER(DecodeParams)]
+    lib.gk_paged_decode_partition_tokens.restype = c_i32
+    lib.gk_paged_decode_partition_tokens.argtypes = [ctypes.POINTER(DecodeParams)]
+    lib.gk_paged_decode.argtypes = [ctypes.POINTER(DecodeParams), c_void_p, ctypes.c_size_t, c_void_p]
+    if hasattr(lib, "gk_paged_prefill"):
+        lib.gk_paged_prefill.argtypes = [ctypes.POINTER(PrefillParams), c_void_p, ctypes.c_size_t, c_void_p]
+        lib.gk_paged_prefill_workspace_bytes.restype = ctypes.c_size_t
+        lib.gk_paged_prefill_workspace_bytes.argtypes = [ctypes.POINTER(PrefillParams)]
+    lib.gk_kv_store.argtypes = [c_void_p, c_void_p, c_i64, c_i64, c_void_p, c_i32, c_void_p, c_i64, c_i32, c_i32,
+                                c_void_p]
+    lib.gk_split_k_merge.argtypes = [c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_i32, c_i32, c_void_p, c_i64,
+                                     c_void_p]
+    lib.gk_attn_tile_indices.argtypes = [c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p]
+    lib.gk_advance_decode_lengths.argtypes = [c_void_p, c_void_p, c_i64, c_void_p, c_void_p, c_void_p]
+    lib.gk_allocator_create.argtypes = [c_i32, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(c_void_p)]
+    lib.gk_allocator_destroy.argtypes = [c_void_p]
+    lib.gk_allocator_alloc.argtypes = [c_void_p, ctypes.c_uint64, c_void_p, ctypes.POINTER(c_void_p)]
+    lib.gk_allocator_record_stream.argtypes = [c_void_p, c_void_p, c_void_p]
+    lib.gk_allocator_free.argtypes = [c_void_p, c_void_p]
+    lib.gk_allocator_empty_cache.argtypes = [c_void_p]
+    lib.gk_allocator_get_stats.argtypes = [c_void_p, ctypes.POINTER(AllocatorStats)]
+    _lib = lib
+    return lib
+
+
+def check(code):
+    if code != GK_OK:
+        raise GkError(code, load().gk_last_error().decode())
+    return code
+
+
+def ptr(tensor):
+    """Device pointer of a tensor (None for None)."""
+    return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
+
+
+def current_stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)

@@ -1,0 +1,125 @@
+// Head-major KV store, tile gather indices and decode-length advance (gfx950).
+//
+// The store scatters each new row's per-head K and V slices into the combined
+// head-major pool. It is pure data movement: every lane moves one 16-byte
+// piece, so a wave writes 1 KiB of contiguous head rows and the kernel runs at
+// the HBM copy rate. Semantics follow gk_kv_store_head_major_bf16_v1 as the
+// reference exercises it (tests/multitile_paged_attention_unit_test.cpp:455-478,
+// tests/fixed_kv_descriptor_device_test.cpp:146-197).
+#include "gk_common.hpp"
+
+namespace gk {
+namespace {
+
+// One thread per 16-byte piece: index = ((row * 2 + kind) * kv_heads + head) * chunks + chunk.
+__global__ __launch_bounds__(256) void kv_store_kernel(const uint16_t* __restrict__ key,
+                                                       const uint16_t* __restrict__ value,
+                                                       int64_t key_stride, int64_t value_stride,
+                                                       const int32_t* __restrict__ slot_mapping,
+                                                       int32_t rows, uint16_t* __restrict__ pool,
+                                                       int64_t slots, int32_t kv_heads, int32_t head_dim) {
+  const int32_t chunks = head_dim >> 3;
+  const int64_t total = (int64_t)rows * 2 * kv_heads * chunks;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t chunk = (int32_t)(i % chunks);
+    int64_t rest = i / chunks;
+    const int32_t head = (int32_t)(rest % kv_heads);
+    rest /= kv_heads;
+    const int32_t kind = (int32_t)(rest & 1);
+    const int32_t row = (int32_t)(rest >> 1);
+    const int32_t slot = slot_mapping[row];
+    if (slot < 0) continue;
+    const uint16_t* src = (kind ? value + row * value_stride : key + row * key_stride) +
+                          (int64_t)head * head_dim + chunk * 8;
+    uint16_t* dst = pool + (((int64_t)kind * kv_heads + head) * slots + slot) * head_dim + chunk * 8;
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+  }
+}
+
+__global__ __launch_bounds__(256) void tile_indices_kernel(const int32_t* __restrict__ mapping,
+                                                           const int32_t* __restrict__ requests,
+                                                           const int32_t* __restrict__ work, int32_t tasks,
+                                                           int32_t context, int32_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)tasks * 64) return;
+  const int32_t t = (int32_t)(i >> 6), l = (int32_t)(i & 63);
+  const int32_t first_row = work[t * 4 + 0], first_key = work[t * 4 + 1];
+  const int32_t lanes = work[t * 4 + 2], base = work[t * 4 + 3];
+  int32_t value = 0;
+  if (lanes > 0) {
+    value = base;
+    if (l < lanes) value += mapping[(int64_t)requests[first_row] * context + first_key + l];
+  }
+  out[i] = value;
+}
+
+__global__ __launch_bounds__(256) void advance_lengths_kernel(const int64_t* __restrict__ seq,
+                                                              const int32_t* __restrict__ orig, int64_t count,
+                                                              int64_t* __restrict__ next,
+                                                              int32_t* __restrict__ orig_next) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  next[i] = seq[i] + 1;
+  orig_next[i] = orig[i] + 1;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+int launch_kv_store(const void* key, const void* value, int64_t key_stride, int64_t value_stride,
+                    const int32_t* slot_mapping, int32_t rows, void* pool, int64_t slots, int32_t kv_heads,
+                    int32_t head_dim, hipStream_t stream) {
+  if (rows < 0 || slots <= 0 || kv_heads <= 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_kv_store: invalid geometry");
+  if (rows == 0) return GK_OK;
+  if (!key || !value || !slot_mapping || !pool)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_kv_store: null pointer");
+  if (!aligned16(key) || !aligned16(value) || !aligned16(pool) || (key_stride & 7) || (value_stride & 7) ||
+      key_stride < (int64_t)kv_heads * head_dim || value_stride < (int64_t)kv_heads * head_dim)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_kv_store: K/V rows must be 16-byte aligned and hold kv_heads * head_dim");
+  const int64_t total = (int64_t)rows * 2 * kv_heads * (head_dim / 8);
+  const int64_t blocks = (total + 255) / 256;
+  const int grid = (int)(blocks < 65536 ? blocks : 65536);
+  kv_store_kernel<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(key), static_cast<const uint16_t*>(value),
+                                            key_stride, value_stride, slot_mapping, rows,
+                                            static_cast<uint16_t*>(pool), slots, kv_heads, head_dim);
+  return hip_status(hipGetLastError(), "gk_kv_store launch");
+}
+
+}  // namespace gk
+
+extern "C" int gk_kv_store(const void* key, const void* value, int64_t key_row_stride, int64_t value_row_stride,
+                           const int32_t* slot_mapping, int32_t rows, void* pool, int64_t slots,
+                           int32_t kv_heads, int32_t head_dim, hipStream_t stream) {
+  gk::clear_error();
+  return gk::launch_kv_store(key, value, key_row_stride, value_row_stride, slot_mapping, rows, pool, slots,
+                             kv_heads, head_dim, stream);
+}
+
+extern "C" int gk_attn_tile_indices(const int32_t* mapping, const int32_t* requests, const int32_t* work,
+                                    int32_t tasks, int32_t context, int32_t* out, hipStream_t stream) {
+  gk::clear_error();
+  if (tasks < 0 || context <= 0) return gk::fail(GK_ERR_INVALID_ARGUMENT, "gk_attn_tile_indices: invalid sizes");
+  if (tasks == 0) return GK_OK;
+  if (!mapping || !requests || !work || !out)
+    return gk::fail(GK_ERR_INVALID_ARGUMENT, "gk_attn_tile_indices: null pointer");
+  const int64_t total = (int64_t)tasks * 64;
+  gk::tile_indices_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(mapping, requests, work, tasks,
+                                                                               context, out);
+  return gk::hip_status(hipGetLastError(), "gk_attn_tile_indices launch");
+}
+
+extern "C" int gk_advance_decode_lengths(const int64_t* seq_lens, const int32_t* orig_seq_lens, int64_t count,
+                                         int64_t* next, int32_t* orig_next, hipStream_t stream) {
+  gk::clear_error();
+  if (count < 0 || count > (int64_t{1} << 30))
+    return gk::fail(GK_ERR_INVALID_ARGUMENT, "gk_advance_decode_lengths: count exceeds supported range");
+  if (count == 0) return GK_OK;
+  if (!seq_lens || !orig_seq_lens || !next || !orig_next)
+    return gk::fail(GK_ERR_INVALID_ARGUMENT, "gk_advance_decode_lengths: null pointer");
+  gk::advance_lengths_kernel<<<(unsigned)((count + 255) / 256), 256, 0, stream>>>(seq_lens, orig_seq_lens, count,
+                                                                                  next, orig_next);
+  return gk::hip_status(hipGetLastError(), "gk_advance_decode_lengths launch");
+}

@@ -1,0 +1,96 @@
+"""Seeded synthetic workloads of the benchmark configurations.
+
+The BASELINE configurations in block-table form: a bf16 head-major pool
+[2, Hkv, S, d] filled with N(0, 1), query rows, seeded non-overlapping block
+tables and seeded lengths. Generated on the GPU with a seeded torch generator.
+"""
+
+import math
+
+import numpy as np
+
+
+def permuted_block_tables(rng, lens, block_size, num_blocks):
+    need = [(int(n) + block_size - 1) // block_size for n in lens]
+    total = sum(need)
+    assert total <= num_blocks, (total, num_blocks)
+    ids = rng.permutation(num_blocks)[:total].astype(np.int32)
+    max_blocks = max(need)
+    table = np.full((len(lens), max_blocks), -1, dtype=np.int32)
+    cursor = 0
+    for b, n in enumerate(need):
+        table[b, :n] = ids[cursor:cursor + n]
+        cursor += n
+    return table
+
+
+# ---------------------------------------------------------------------------
+# Full-size configurations (generated on the GPU; need torch + a device)
+# ---------------------------------------------------------------------------
+
+CONFIGS = {
+    # name: (batch, heads, kv_heads, head_dim, block, pool_blocks, length sampler)
+    "c2": (64, 32, 8, 128, 128, 4096, lambda rng, b: rng.integers(512, 4097, b)),
+    "c3": (256, 32, 8, 128, 128, None, lambda rng, b: rng.integers(128, 2049, b)),
+    "c5": (32, 64, 8, 128, 128, 8192,
+           lambda rng, b: np.rint(np.exp(rng.uniform(math.log(1024), math.log(32768), b))).astype(np.int64)),
+}
+
+
+class DeviceDecodeCase:
+    """A decode problem whose pool and queries live on the GPU (torch tensors)."""
+
+    def __init__(self, name, seed=1234, device="cuda"):
+        import torch
+
+        batch, heads, kv_heads, d, block, pool_blocks, sampler = CONFIGS[name]
+        rng = np.random.default_rng(seed)
+        lens = np.asarray(sampler(rng, batch), dtype=np.int32)
+        self.name = name
+        self.store = name == "c3"
+        # c3 attends len + 1 keys: the new token sits at position len.
+        self.lens = lens + 1 if self.store else lens
+        need = (self.lens.astype(np.int64) + block - 1) // block
+        if pool_blocks is None:
+            pool_blocks = int(need.sum())
+        self.batch, self.heads, self.kv_heads, self.head_dim, self.block_size = batch, heads, kv_heads, d, block
+        self.scale = float(np.float32(1 / math.sqrt(d)))
+        self.tables = permuted_block_tables(rng, self.lens, block, pool_blocks)
+        self.slots = pool_blocks * block
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        self.pool = torch.empty((2, kv_heads, self.slots, d), dtype=torch.bfloat16, device=device)
+        for kind in range(2):
+            for h in range(kv_heads):
+                self.pool[kind, h].normal_(generator=gen)
+        self.query = torch.randn((batch, heads * d), generator=gen, device=device).to(torch.bfloat16)
+        self.d_tables = torch.from_numpy(self.tables).to(device)
+        self.d_lens = torch.from_numpy(self.lens).to(device)
+        if self.store:
+            pos = lens.astype(np.int64)
+            self.slot_mapping = (self.tables[np.arange(batch), pos // block].astype(np.int64) * block + pos % block)
+            self.d_slot_mapping = torch.from_numpy(self.slot_mapping.astype(np.int32)).to(device)
+            self.new_key = torch.randn((batch, kv_heads * d), generator=gen, device=device).to(torch.bfloat16)
+            self.new_value = torch.randn((batch, kv_heads * d), generator=gen, device=device).to(torch.bfloat16)
+        self.out = torch.empty((batch, heads * d), dtype=torch.bfloat16, device=device)
+
+    def kv_bytes(self):
+        return int(self.lens.astype(np.int64).sum()) * self.kv_heads * self.head_dim * 2 * 2
+
+    def step_bytes(self):
+        """Algorithmic HBM bytes of one step: K/V rows read, Q read, O written, tables and lengths,
+        plus the store's read and write of the new rows when the case stores."""
+        b = self.kv_bytes()
+        b += 2 * self.batch * self.heads * self.head_dim * 2
+        b += int(((self.lens.astype(np.int64) + self.block_size - 1) // self.block_size).sum()) * 4 + 4 * self.batch
+        if self.store:
+            b += 2 * 2 * self.batch * self.kv_heads * self.head_dim * 2 + 4 * self.batch
+        return b
+
+    def host_arrays(self):
+        """(query, pool) copied back as uint16 bf16 bits, after any store has run."""
+        import torch
+
+        pool = self.pool.view(torch.int16).cpu().numpy().view(np.uint16)
+        query = self.query.view(torch.int16).cpu().numpy().view(np.uint16)
+        return query, pool

@@ -1,0 +1,164 @@
+/*
+ * gaudirt_amd — C ABI of the MI355X (gfx950) paged-attention path.
+ *
+ * Every entry point takes plain pointers, sizes and a hipStream_t, enqueues its
+ * work on that stream and returns a status code (GK_OK on success); no C++
+ * exception crosses this boundary. On failure gk_last_error() returns a
+ * message for the calling thread. Arguments are validated on the host before
+ * anything is enqueued, so a rejected call has written nothing.
+ *
+ * KV pool layout (the reference's head-major combined pool, one layer):
+ *   bf16 [2, kv_heads, slots, head_dim]; key row of (head h, slot s) at
+ *   element (h * slots + s) * head_dim, value row at
+ *   ((kv_heads + h) * slots + s) * head_dim.
+ * Block tables: block_tables[request * bt_stride + j] is the pool block that
+ * holds tokens [j * block_size, (j + 1) * block_size) of the request, so token
+ * t lives at slot block_tables[...t / block_size] * block_size + t % block_size.
+ * block_size is a power of two; block_size 1 makes the table the reference's
+ * token-granular request map (mapping[request, token] = slot).
+ */
+#ifndef GAUDIRT_AMD_H
+#define GAUDIRT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  GK_OK = 0,
+  GK_ERR_INVALID_ARGUMENT = 1,
+  GK_ERR_UNSUPPORTED = 2,
+  GK_ERR_HIP = 3,
+  GK_ERR_OUT_OF_MEMORY = 4,
+  GK_ERR_WORKSPACE = 5,
+};
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* gk_last_error(void);
+/* Library version string. */
+const char* gk_version(void);
+
+/* ---------------------------------------------------------------------------
+ * KV store. Replaces the gk_kv_store_head_major_bf16_v1 launch of
+ * src/bridge/paged_attention_tiles.cpp:266-290 (recipe :67-85, fused variant
+ * src/bridge/paged_attention.cpp:66-76): for r < rows and every kv head, the
+ * row's head slice of key/value is written to slot slot_mapping[r] of the pool.
+ * A negative slot skips the row; every other pool byte is untouched.
+ * key/value: bf16 [rows, kv_row_stride] (elements), kv_heads * head_dim used.
+ * ------------------------------------------------------------------------- */
+int gk_kv_store(const void* key, const void* value, int64_t key_row_stride, int64_t value_row_stride,
+                const int32_t* slot_mapping, int32_t rows, void* pool, int64_t slots, int32_t kv_heads,
+                int32_t head_dim, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged decode attention over block tables with split-K partitions and a
+ * second-pass log-sum-exp merge. Replaces the fused single-tile recipe and the
+ * multi-tile chunk chain of src/bridge/paged_attention.cpp:39-127,264-345 and
+ * src/bridge/paged_attention_tiles.cpp:87-225,292-389 (tile softmax,
+ * gk_attn_online_merge_f32_v1, gk_attn_online_finalize_bf16_v1).
+ *
+ * Each query row r attends keys [left, row_context[r]) of request
+ * row_request[r], where left = max(0, row_context[r] - sliding_window) when a
+ * window is set and 0 otherwise. Scores are q.k in fp32 times `scale`
+ * (optionally capped: softcap * tanh(s / softcap)); output bf16.
+ * ------------------------------------------------------------------------- */
+typedef struct gk_decode_params {
+  const void* query;           /* bf16 [rows, q_row_stride]; heads contiguous in a row */
+  int64_t q_row_stride;        /* elements */
+  const void* pool;            /* head-major combined KV pool of one layer */
+  int64_t slots;
+  const int32_t* block_tables; /* [requests, bt_stride] */
+  int64_t bt_stride;
+  int32_t block_size;          /* power of two */
+  const int32_t* row_request;  /* [rows] block-table row of each query row; NULL = row index */
+  const int32_t* row_context;  /* [rows] visible keys (query position + 1) */
+  int32_t rows;
+  int32_t q_heads, kv_heads, head_dim; /* head_dim in {64, 128, 256}; q_heads % kv_heads == 0 */
+  float scale;
+  float softcap;               /* 0 = off */
+  int32_t sliding_window;      /* <= 0 = off */
+  int32_t max_context;         /* host bound: row_context[r] <= max_context for every row */
+  int32_t partition_tokens;    /* split-K partition (multiple of 32); 0 = library choice */
+  void* out;                   /* bf16 [rows, out_row_stride] */
+  int64_t out_row_stride;      /* elements */
+  /* Optional fused KV store of the new token rows (NULL new_key = none): written
+   * with gk_kv_store semantics before any key is read. */
+  const void* new_key;
+  const void* new_value;
+  int64_t new_kv_row_stride;
+  const int32_t* slot_mapping;
+} gk_decode_params;
+
+/* Workspace bytes gk_paged_decode needs for these parameters (0 if none). */
+size_t gk_paged_decode_workspace_bytes(const gk_decode_params* params);
+/* The split-K partition gk_paged_decode uses for these parameters. */
+int32_t gk_paged_decode_partition_tokens(const gk_decode_params* params);
+int gk_paged_decode(const gk_decode_params* params, void* workspace, size_t workspace_bytes,
+                    hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Split-K merge on its own: combines `parts` fp32 partial states per (row, head)
+ * into bf16 output. partial_out [rows, heads, max_parts, head_dim] holds
+ * unnormalised sums sum_t 2^(s_t - m) v_t; partial_ml [rows, heads, max_parts, 2]
+ * holds (m, l) with m in log2 units and l = sum_t 2^(s_t - m); part_count[r] is
+ * the number of valid parts of row r. Replaces gk_attn_online_merge_f32_v1 and
+ * gk_attn_online_finalize_bf16_v1 (src/bridge/paged_attention_tiles.cpp:164-190).
+ * ------------------------------------------------------------------------- */
+int gk_split_k_merge(const float* partial_out, const float* partial_ml, const int32_t* part_count,
+                     int32_t rows, int32_t heads, int32_t max_parts, int32_t head_dim, void* out,
+                     int64_t out_row_stride, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Tile gather indices in the reference's format (gk_attn_tile_indices_i32_v1,
+ * src/bridge/attention_plan.cpp:36-57,337-354): task t = {first_row, first_key,
+ * lanes, base} int32 x4; out[t * 64 + l] = base + mapping[requests[first_row] *
+ * context + first_key + l] for l < lanes, base for the other lanes of a partial
+ * task and 0 for a task with no lane.
+ * ------------------------------------------------------------------------- */
+int gk_attn_tile_indices(const int32_t* mapping, const int32_t* requests, const int32_t* work,
+                         int32_t tasks, int32_t context, int32_t* out, hipStream_t stream);
+
+/* Decode-length advance (src/bridge/eager_scheduler.cpp:50-82): next = seq + 1
+ * (int64) and orig_next = orig + 1 (int32) in one launch. */
+int gk_advance_decode_lengths(const int64_t* seq_lens, const int32_t* orig_seq_lens, int64_t count,
+                              int64_t* next, int32_t* orig_next, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Stream-ordered block allocator (replaces runtime::BlockCachingAllocator,
+ * include/gaudirt/runtime/block_caching_allocator.hpp:19-70, for this path).
+ * HBM slabs from hipMalloc, carved into 256-byte aligned blocks by best fit.
+ * A block freed after use on other streams is reused on a stream only after
+ * that stream waits on events recorded on them (no host synchronisation);
+ * events come from a pool, so steady state creates none.
+ * ------------------------------------------------------------------------- */
+typedef struct gk_allocator gk_allocator;
+
+typedef struct gk_allocator_stats {
+  uint64_t allocated_bytes;
+  uint64_t peak_bytes;
+  uint64_t reserved_bytes;
+  uint64_t largest_free_block;
+  uint64_t slabs;
+  uint64_t events_created;
+} gk_allocator_stats;
+
+/* budget_bytes caps the total slab bytes; slab_bytes is the default slab size. */
+int gk_allocator_create(int32_t device, uint64_t budget_bytes, uint64_t slab_bytes, gk_allocator** out);
+int gk_allocator_destroy(gk_allocator* allocator);
+int gk_allocator_alloc(gk_allocator* allocator, uint64_t bytes, hipStream_t stream, void** out);
+int gk_allocator_record_stream(gk_allocator* allocator, void* ptr, hipStream_t stream);
+int gk_allocator_free(gk_allocator* allocator, void* ptr);
+/* Waits for pending reuse fences and returns fully free slabs to HIP. */
+int gk_allocator_empty_cache(gk_allocator* allocator);
+int gk_allocator_get_stats(gk_allocator* allocator, gk_allocator_stats* stats);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GAUDIRT_AMD_H */

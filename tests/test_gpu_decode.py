@@ -1,0 +1,137 @@
+"""GPU parity of the decode path (C ABI) against the CPU oracle.
+
+Tolerance: bf16 outputs within max-abs 2e-2 and mean-abs
+2e-3 of the reference implementation (direct_bf16_pv, and tiled_bf16_pv with
+the reference's 512-key tile), plus the reference's own relative-L2 gates
+(<= 1e-2 vs fp64, <= 5e-3 vs tiled; tests/paged_attention_reference.py:60-69).
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import paged_cases as cases
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def check_against_oracle(case, actual_bits, threads=16):
+    p = case.oracle_problem()
+    direct = orc.direct_bf16_pv(p, threads)
+    tiled = orc.tiled_bf16_pv(p, 512, threads)
+    fp64 = orc.fp64_bf16(p, threads)
+    assert np.isfinite(orc.bf16_to_f32(actual_bits)).all()
+    for name, ref in (("direct_bf16_pv", direct), ("tiled_bf16_pv", tiled)):
+        max_abs, mean_abs = orc.tolerance_errors(actual_bits, ref)
+        print(f"{name}: max_abs={max_abs:.3e} mean_abs={mean_abs:.3e}", flush=True)
+        assert max_abs <= MAX_ABS and mean_abs <= MEAN_ABS, (name, max_abs, mean_abs)
+    e64, etiled = orc.isolated_errors(orc.bf16_to_f32(actual_bits), fp64, orc.bf16_to_f32(tiled))
+    print(f"isolated_errors: fp64={e64:.3e} tiled={etiled:.3e}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def runner():
+    import torch
+    assert torch.cuda.is_available()
+    from tests import gk_runner
+    return gk_runner
+
+
+def test_c1_decode(runner):
+    case = cases.c1_case()
+    print("c1 lens", case.lens.tolist(), flush=True)
+    check_against_oracle(case, runner.run_case(case))
+
+
+@pytest.mark.parametrize("partition", [32, 64, 128, 512])
+def test_c1_decode_split_k_partitions(runner, partition):
+    case = cases.c1_case(seed=77)
+    check_against_oracle(case, runner.run_case(case, partition=partition))
+
+
+@pytest.mark.parametrize("geometry", [(8, 8, 64), (14, 2, 64), (56, 8, 128), (9, 3, 64), (16, 8, 256), (64, 8, 128),
+                                      (8, 1, 256), (32, 2, 128)])
+def test_decode_geometries(runner, geometry):
+    heads, kv_heads, d = geometry
+    rng = np.random.default_rng(heads * 1000 + kv_heads * 10 + d)
+    lens = np.concatenate([[1, 2, 31, 32, 33, 127, 128, 129], rng.integers(1, 1500, 4)])
+    case = cases.decode_case(7, len(lens), heads, kv_heads, d, 16, 1024, lens)
+    print("geometry", geometry, flush=True)
+    check_against_oracle(case, runner.run_case(case, partition=256))
+
+
+@pytest.mark.parametrize("block_size", [1, 8, 64, 256])
+def test_block_sizes(runner, block_size):
+    lens = np.array([5, 300, 777, 1024, 63])
+    case = cases.decode_case(block_size, len(lens), 16, 4, 128, block_size, 4096 // block_size * 2, lens)
+    check_against_oracle(case, runner.run_case(case, partition=128))
+
+
+def test_softcap_and_window(runner):
+    lens = np.array([40, 300, 1000, 64, 65])
+    case = cases.decode_case(99, len(lens), 8, 4, 256, 32, 256, lens)
+    case.softcap, case.window = 50.0, 64
+    actual = runner.run_case(case, partition=64)
+    ref = orc.fp32_softmax_attention(case.oracle_problem())
+    max_abs, mean_abs = orc.tolerance_errors(actual, ref)
+    assert max_abs <= MAX_ABS and mean_abs <= MEAN_ABS, (max_abs, mean_abs)
+
+
+def test_poisoned_unused_slots_do_not_propagate(runner):
+    # Slots outside every visible prefix hold NaN; masked lanes read slot 0.
+    lens = np.array([3, 50, 129])
+    case = cases.decode_case(5, len(lens), 8, 2, 128, 16, 64, lens)
+    used = np.zeros(case.slots, dtype=bool)
+    for b, n in enumerate(case.lens):
+        for t in range(n):
+            used[case.block_tables[b, t // 16] * 16 + t % 16] = True
+    case.pool[:, :, ~used, :] = 0x7fc0
+    actual = runner.run_case(case, partition=32)
+    check_against_oracle(case, actual)
+
+
+@pytest.mark.parametrize("name", ["c2", "c5"])
+def test_full_size_decode(runner, name):
+    import torch
+    from gaudirt_amd import workloads
+
+    dc = workloads.DeviceDecodeCase(name)
+    print(name, "lens min/mean/max", dc.lens.min(), dc.lens.mean(), dc.lens.max(), flush=True)
+    params = runner.decode_params(dc.query, dc.pool, dc.d_tables, dc.d_lens, dc.heads, dc.kv_heads, dc.head_dim,
+                                  dc.block_size, dc.scale, dc.out)
+    ws = runner.paged_decode(params)
+    torch.cuda.synchronize()
+    del ws
+    actual = runner.bits_of(dc.out)
+    check_against_oracle(cases.host_case(dc), actual)
+
+
+def test_c3_fused_store_then_decode(runner):
+    import torch
+    from gaudirt_amd import workloads
+
+    dc = workloads.DeviceDecodeCase("c3")
+    before = dc.pool.clone()
+    params = runner.decode_params(dc.query, dc.pool, dc.d_tables, dc.d_lens, dc.heads, dc.kv_heads, dc.head_dim,
+                                  dc.block_size, dc.scale, dc.out, new_key=dc.new_key, new_value=dc.new_value,
+                                  slot_mapping=dc.d_slot_mapping)
+    ws = runner.paged_decode(params)
+    torch.cuda.synchronize()
+    del ws
+    # Store: bit-exact at the targeted slots, every other byte untouched.
+    slots = torch.from_numpy(dc.slot_mapping).cuda()
+    touched = torch.zeros(dc.slots, dtype=torch.bool, device="cuda")
+    touched[slots] = True
+    for kind, rows in ((0, dc.new_key), (1, dc.new_value)):
+        for h in range(dc.kv_heads):
+            got = dc.pool[kind, h][slots].view(torch.int16)
+            want = rows[:, h * dc.head_dim:(h + 1) * dc.head_dim].view(torch.int16)
+            assert torch.equal(got, want), (kind, h)
+            assert torch.equal(dc.pool[kind, h][~touched].view(torch.int16),
+                               before[kind, h][~touched].view(torch.int16)), (kind, h)
+    del before
+    check_against_oracle(cases.host_case(dc), runner.bits_of(dc.out))
