@@ -1,0 +1,210 @@
+"""Paged decode attention benchmark on one MI355X (gfx950).
+
+One step = one gk_paged_decode call (C ABI) over the whole batch of the
+workload: every sequence's new query row attends its paged K/V through the
+block tables, split-K partitions plus log-sum-exp merge, bf16 output. Inputs
+(pool, queries, block tables, lengths) are resident in HBM before timing
+starts. Consecutive steps rotate over `--table-sets` disjoint block-table sets
+of the same pool (same lengths, different blocks), so a step cannot be served
+from the 256 MB last-level cache that the previous step filled.
+
+Prints ONE JSON line: value = decode tokens/s (sequences per second of one
+layer's attention step), the HBM roofline of the decode kernel measured with
+HIP events on the launch stream, and the CPU baseline (the C oracle, a
+restatement of the reference's direct_bf16_pv, on the host's cores).
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload c2] [--no-cpu]
+"""
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decode attn tokens/s + achieved KV-read HBM GB/s (% of 8 TB/s), 1 MI355X"
+HBM_PEAK_GBPS = 8000.0
+
+WORKLOADS = {
+    "c2": "Llama-3-8B-shaped paged decode: batch 64, 32 q / 8 kv heads, head_dim 128, block 128, "
+          "ctx U[512,4096], 4096-block bf16 pool",
+    "c3": "fused KV store + decode: batch 256, 32 q / 8 kv heads, head_dim 128, block 128, len U[128,2048]",
+    "c5": "70B-shaped long decode: batch 32, 64 q / 8 kv heads, head_dim 128, block 128, "
+          "ctx log-U[1024,32768], 8192-block pool, split-K",
+}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--table-sets", type=int, default=3)
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = library choice)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
+    return ap.parse_args()
+
+
+def cpu_baseline(dc, target_seconds):
+    """Time the C oracle's direct_bf16_pv (reference restatement) on a bounded sample of the batch."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    query, pool = dc.host_arrays()
+    context = int(dc.lens.max())
+    mapping = orc.mapping_from_block_table(dc.tables, dc.block_size, context)
+
+    def run(rows):
+        p = orc.Problem(query[:rows], pool, np.arange(rows), dc.lens[:rows].astype(np.int64) - 1, mapping,
+                        dc.heads, dc.kv_heads, dc.head_dim, dc.scale)
+        t0 = time.perf_counter()
+        orc.direct_bf16_pv(p, threads)
+        return time.perf_counter() - t0
+
+    probe_rows = min(dc.batch, threads)
+    probe = run(probe_rows)
+    full = probe * dc.batch / probe_rows  # estimated seconds for the whole batch
+    rows = dc.batch
+    reps = max(1, min(50, int(target_seconds / max(full, 1e-6))))
+    if full > target_seconds:
+        rows = max(probe_rows, min(dc.batch, int(probe_rows * target_seconds / max(probe, 1e-6))))
+        reps = 1
+    times = [run(rows) for _ in range(reps)]
+    t = statistics.median(times)
+    kv_tokens = int(dc.lens[:rows].astype(np.int64).sum())
+    return {
+        "value": rows / t,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"first {rows} of {dc.batch} sequences ({kv_tokens} KV tokens), direct_bf16_pv C oracle, "
+                  f"median of {reps} run(s), {t:.3f} s each",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the decode path does not shard across GPUs here", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from gaudirt_amd import capi, workloads
+
+    assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    torch.cuda.set_device(0)
+    lib = capi.load()
+    dc = workloads.DeviceDecodeCase(args.workload, seed=args.seed, table_sets=args.table_sets)
+    stream = torch.cuda.current_stream()
+    hstream = ctypes.c_void_p(stream.cuda_stream)
+
+    params = []
+    for i, tables in enumerate(dc.d_table_sets):
+        p = capi.DecodeParams()
+        p.query, p.q_row_stride = dc.query.data_ptr(), dc.query.stride(0)
+        p.pool, p.slots = dc.pool.data_ptr(), dc.slots
+        p.block_tables, p.bt_stride, p.block_size = tables.data_ptr(), tables.stride(0), dc.block_size
+        p.row_request, p.row_context, p.rows = None, dc.d_lens.data_ptr(), dc.batch
+        p.q_heads, p.kv_heads, p.head_dim = dc.heads, dc.kv_heads, dc.head_dim
+        p.scale, p.softcap, p.sliding_window = dc.scale, 0.0, -1
+        p.max_context, p.partition_tokens = int(dc.lens.max()), args.partition
+        p.out, p.out_row_stride = dc.out.data_ptr(), dc.out.stride(0)
+        if dc.store:
+            p.new_key, p.new_value = dc.new_key.data_ptr(), dc.new_value.data_ptr()
+            p.new_kv_row_stride = dc.new_key.stride(0)
+            p.slot_mapping = dc.d_slot_mappings[i].data_ptr()
+        params.append(p)
+    need = max(lib.gk_paged_decode_workspace_bytes(ctypes.byref(p)) for p in params)
+    workspace = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    partition = lib.gk_paged_decode_partition_tokens(ctypes.byref(params[0]))
+
+    def step(i):
+        capi.check(lib.gk_paged_decode(ctypes.byref(params[i % len(params)]),
+                                       ctypes.c_void_p(workspace.data_ptr()), need, hstream))
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    start.record(stream)
+    for i in range(args.steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    step_bytes = dc.step_bytes()
+    kv_bytes = dc.kv_bytes()
+    seconds = ms_per_step * 1e-3
+    achieved = step_bytes / seconds / 1e9
+    tokens_per_s = dc.batch / seconds
+    print(f"[bench] {args.workload}: {ms_per_step * 1e3:.1f} us/step, {tokens_per_s:.4g} tokens/s, "
+          f"{achieved:.1f} GB/s ({achieved / HBM_PEAK_GBPS:.1%} of peak), KV {kv_bytes / 1e9:.4f} GB/step, "
+          f"partition {partition}, wall {wall:.2f} s", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(dc, args.cpu_seconds)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": METRIC,
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: {WORKLOADS[args.workload]}",
+            "batch": dc.batch,
+            "q_heads": dc.heads,
+            "kv_heads": dc.kv_heads,
+            "head_dim": dc.head_dim,
+            "block_size": dc.block_size,
+            "mean_context": float(dc.lens.mean()),
+            "max_context": int(dc.lens.max()),
+            "split_k_partition": int(partition),
+            "table_sets": len(params),
+            "seed": args.seed,
+            "kv_read_gbps": kv_bytes / seconds / 1e9,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -93,8 +93,7 @@ def build_extension():
 
 def build(jobs=8):
     lib = build_library(jobs)
-    ext = build_extension()
-    return lib, ext
+    return (lib,)
 
 
 if __name__ == "__main__":

@@ -7,10 +7,12 @@ library has not been built; there is no other implementation behind it.
 """
 
 import ctypes
+import os
 import pathlib
 
 PACKAGE = pathlib.Path(__file__).resolve().parent
-LIB_PATH = PACKAGE / "libgaudirt_amd.so"
+# GAUDIRT_AMD_LIB selects another build of the same library (e.g. a tuning variant).
+LIB_PATH = pathlib.Path(os.environ.get("GAUDIRT_AMD_LIB", PACKAGE / "libgaudirt_amd.so"))
 
 GK_OK = 0
 GK_ERR_INVALID_ARGUMENT = 1
@@ -19,11 +21,11 @@ GK_ERR_HIP = 3
 GK_ERR_OUT_OF_MEMORY = 4
 GK_ERR_WORKSPACE = 5
 
-# Every function include/gaudirt_amd.h declares (checked by tests/test_capi.py).
+# Every function include/gaudirt_amd.h declares.
 EXPORTED = [
     "gk_last_error", "gk_version", "gk_kv_store", "gk_paged_decode_workspace_bytes",
-    "gk_paged_decode_partition_tokens", "gk_paged_decode", "gk_split_k_merge", "gk_paged_prefill",
-    "gk_paged_prefill_workspace_bytes", "gk_attn_tile_indices", "gk_advance_decode_lengths",
+    "gk_paged_decode_partition_tokens", "gk_paged_decode", "gk_split_k_merge",
+    "gk_attn_tile_indices", "gk_advance_decode_lengths",
     "gk_allocator_create", "gk_allocator_destroy", "gk_allocator_alloc", "gk_allocator_record_stream",
     "gk_allocator_free", "gk_allocator_empty_cache", "gk_allocator_get_stats",
 ]
@@ -46,19 +48,6 @@ class DecodeParams(ctypes.Structure):
         ("out", c_void_p), ("out_row_stride", c_i64),
         ("new_key", c_void_p), ("new_value", c_void_p), ("new_kv_row_stride", c_i64),
         ("slot_mapping", c_void_p),
-    ]
-
-
-class PrefillParams(ctypes.Structure):
-    _fields_ = [
-        ("query", c_void_p), ("q_row_stride", c_i64),
-        ("pool", c_void_p), ("slots", c_i64),
-        ("block_tables", c_void_p), ("bt_stride", c_i64), ("block_size", c_i32),
-        ("seq_request", c_void_p), ("seq_prefix", c_void_p), ("seq_rows", c_void_p),
-        ("seq_first_row", c_void_p), ("seqs", c_i32), ("max_rows", c_i32),
-        ("q_heads", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32),
-        ("scale", c_f32), ("softcap", c_f32), ("sliding_window", c_i32),
-        ("out", c_void_p), ("out_row_stride", c_i64),
     ]
 
 
@@ -91,10 +80,6 @@ def load():
     lib.gk_paged_decode_partition_tokens.restype = c_i32
     lib.gk_paged_decode_partition_tokens.argtypes = [ctypes.POINTER(DecodeParams)]
     lib.gk_paged_decode.argtypes = [ctypes.POINTER(DecodeParams), c_void_p, ctypes.c_size_t, c_void_p]
-    if hasattr(lib, "gk_paged_prefill"):
-        lib.gk_paged_prefill.argtypes = [ctypes.POINTER(PrefillParams), c_void_p, ctypes.c_size_t, c_void_p]
-        lib.gk_paged_prefill_workspace_bytes.restype = ctypes.c_size_t
-        lib.gk_paged_prefill_workspace_bytes.argtypes = [ctypes.POINTER(PrefillParams)]
     lib.gk_kv_store.argtypes = [c_void_p, c_void_p, c_i64, c_i64, c_void_p, c_i32, c_void_p, c_i64, c_i32, c_i32,
                                 c_void_p]
     lib.gk_split_k_merge.argtypes = [c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_i32, c_i32, c_void_p, c_i64,

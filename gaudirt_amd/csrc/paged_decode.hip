@@ -1,20 +1,30 @@
 // Paged decode attention for gfx950: split-K partitions + log-sum-exp merge.
 //
-// Work decomposition. One workgroup of NW waves owns one (query row, kv head,
-// head group, partition of `partition` keys). The G query heads that share a
-// kv head are computed together, so each K/V byte is read from HBM once per
-// group. Decode has no dense contraction to feed MFMA (M = G <= 8 rows), so
-// Q.K and P.V run as wave-level bf16 dot2 (v_dot2_f32_bf16) with fp32
-// accumulation.
+// Work decomposition. A work item is one (query row, kv head, head group,
+// partition of `partition` keys). The query heads that share a kv head are
+// computed together, so each K/V byte is read from HBM once per group. The
+// partition's block-table entries are staged in LDS first, so no K/V load ever
+// waits on another load (a block-table lookup is an LDS read).
 //
-// Lane layout. A head row of D bf16 (2*D bytes) is split over LPT = D/16 lanes;
-// lane j of a token group owns d in [8j, 8j+8) and [D/2 + 8j, D/2 + 8j + 8).
-// One load instruction therefore covers TPW = 64/LPT consecutive tokens times a
-// contiguous half row (128 B for D = 128): every cache line fetched is used in
-// full. Q.K partial sums are reduced over the LPT lanes with DPP; the token
-// group keeps its own running max/sum/output (online softmax), P.V needs no
-// cross-lane traffic, and the groups, then the waves, are merged once at the
-// end (registers, then LDS).
+// Two kernels compute a partition:
+//
+//  * decode_mfma_kernel (GQA group >= 4, head_dim 64/128/256): one wave per
+//    work item. The group's query heads are the 16 rows of bf16 MFMA tiles.
+//    Scores are computed transposed, S^T[token][head] = K . Q^T with
+//    v_mfma_f32_16x16x32_bf16, which leaves each lane holding one head's
+//    scores for 8 tokens: exactly the A operand of the P.V MFMA, so
+//    probabilities never move between lanes. K goes from HBM straight into
+//    MFMA operand registers with 16-byte buffer loads. V is loaded the same
+//    way, written to LDS row-major with its 16-byte chunks XOR-swizzled by
+//    token, and read back transposed with ds_read_b64_tr_b16 as the B operand
+//    [token][dim] of P.V.
+//
+//  * decode_dot_kernel (groups 1..3, where a 16-row MFMA tile would be mostly
+//    padding): a workgroup of four waves per work item. Q.K and P.V run as
+//    wave-level bf16 dot2 (v_dot2_f32_bf16) with fp32 accumulation. A head row
+//    of D bf16 is split over LPT = D/16 lanes; one load instruction covers
+//    TPW = 64/LPT consecutive tokens, so every cache line fetched is used in
+//    full. The waves' partial states are merged through LDS.
 //
 // Partial results (unnormalised fp32 output and (max, sum) in log2 units) go to
 // the workspace; a second kernel merges the partitions of each row with the
@@ -33,6 +43,16 @@ namespace gk {
 namespace {
 
 constexpr int kWaves = 4;
+// Waves per SIMD the MFMA kernel is compiled for: 3 bounds its registers to
+// 168 (head_dim <= 128); head_dim 256 holds twice the accumulators and gets 2.
+#ifndef GK_MFMA_WAVES_PER_SIMD
+#define GK_MFMA_WAVES_PER_SIMD 3
+#endif
+template <int D>
+constexpr int mfma_waves_per_simd() { return D == 256 ? 2 : GK_MFMA_WAVES_PER_SIMD; }
+// The MFMA kernel re-bases its running max only when a score exceeds it by more
+// than this (log2 units): probabilities stay <= 2^8 and rescales are rare.
+constexpr float kLazyRescale = 8.f;
 
 struct DecodeArgs {
   const uint16_t* query;
@@ -44,7 +64,7 @@ struct DecodeArgs {
   int32_t block_shift;
   const int32_t* row_request;
   const int32_t* row_context;
-  int32_t rows, q_heads, kv_heads, group, head_groups;
+  int32_t rows, q_heads, kv_heads, group, head_groups, heads_per_group;
   float score_scale;  // scale * log2(e), or scale / softcap when capping
   float softcap_log2; // softcap * log2(e) when capping
   int32_t window, partition, max_parts;
@@ -70,8 +90,355 @@ __device__ __forceinline__ int visible_left(int ctx, int window) {
   return (window > 0 && ctx > window) ? ctx - window : 0;
 }
 
+// Partition bounds shared by both kernels: keys [t_begin, t_end) of the row.
+struct PartitionRange {
+  int t_begin, t_end, nparts;
+};
+
+__device__ __forceinline__ PartitionRange partition_range(const DecodeArgs& a, int ctx, int part) {
+  const int left = visible_left(ctx, a.window);
+  const int span = ctx > left ? ctx - left : 0;
+  PartitionRange r;
+  r.nparts = (span + a.partition - 1) / a.partition;
+  r.t_begin = left + part * a.partition;
+  r.t_end = min(r.t_begin + a.partition, ctx);
+  return r;
+}
+
+// Stage the block-table entries covering keys [t_begin, t_end) in LDS:
+// s_bt[i] = block id of block (t_begin >> shift) + i. Ends with a barrier.
+__device__ __forceinline__ int stage_block_ids(const DecodeArgs& a, const int32_t* __restrict__ bt, int t_begin,
+                                               int t_end, int32_t* s_bt) {
+  const int b0 = t_begin >> a.block_shift;
+  const int nblk = t_end > t_begin ? ((t_end - 1) >> a.block_shift) - b0 + 1 : 0;
+  for (int i = threadIdx.x; i < nblk; i += blockDim.x) s_bt[i] = bt[b0 + i];
+  __syncthreads();
+  return b0;
+}
+
+__device__ __forceinline__ int slot_of(const int32_t* s_bt, int b0, int shift, int t) {
+  return (s_bt[(t >> shift) - b0] << shift) | (t & ((1 << shift) - 1));
+}
+
+// ---------------------------------------------------------------------------
+// MFMA kernel
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+// Word 3 of a raw buffer resource on gfx950 (32-bit data format, offset mode).
+constexpr int kBufferDword3 = 0x00020000;
+
+template <int D>
+struct MfmaShape {
+  static constexpr int TS = D == 256 ? 16 : 32;   // keys per step
+  static constexpr int TG = TS / 16;              // 16-key groups per step (QK tiles)
+  static constexpr int NC = D / 32;               // 32-dim k chunks of Q.K
+  static constexpr int CPR = D / 8;               // 16-byte chunks per head row
+  static constexpr int LOADS = TS * CPR / 64;     // 16-byte loads per lane per tile
+  static constexpr int NO = D / 16;               // 16-dim output chunks of P.V
+  static constexpr int TILE = TS * D * 2;         // bytes of one K or V tile in LDS
+};
+
+// Token swizzle of 16-byte chunks inside an LDS row: chunk c of token t is
+// stored at c ^ swz(t). Conflict-free both for the row-major tile writes and
+// for the transposed 4-token reads of P.V.
+__device__ __forceinline__ int swz(int t) { return ((t & 3) << 1) | ((t >> 2) & 1); }
+
+// Wait until at most N vector memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ f32x4_t mfma32(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma16(const bf16x4_t& a, const bf16x4_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, a), __builtin_bit_cast(i16x4_t, b), c,
+                                                   0, 0, 0);
+}
+
+// One wave per workgroup; the workgroup owns (partition blockIdx.x, kv head /
+// head group blockIdx.y, query row blockIdx.z). Waves never synchronise with
+// each other: partitions are uniform in size, so the GPU stays evenly loaded
+// however skewed the context lengths are, and the log-sum-exp merge combines
+// a row's partitions afterwards.
+template <int D, bool SOFTCAP>
+__global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kernel(DecodeArgs a) {
+  using S = MfmaShape<D>;
+  // Two stages of K and V tiles (separate objects, so the compiler can tell a
+  // stage's reads from the other stage's loads in flight).
+  __shared__ __attribute__((aligned(16))) char kt0[S::TILE];
+  __shared__ __attribute__((aligned(16))) char vt0[S::TILE];
+  __shared__ __attribute__((aligned(16))) char kt1[S::TILE];
+  __shared__ __attribute__((aligned(16))) char vt1[S::TILE];
+  extern __shared__ int32_t s_bt[];
+
+  const int lane = threadIdx.x;
+  const int q = lane >> 4, c16 = lane & 15;
+  const int row = blockIdx.z;
+  const int kvh = blockIdx.y / a.head_groups, hg = blockIdx.y % a.head_groups;
+  const int ctx = a.row_context[row];
+  const PartitionRange pr = partition_range(a, ctx, blockIdx.x);
+  if ((int)blockIdx.x >= (pr.nparts > 1 ? pr.nparts : 1)) return;
+  const int request = a.row_request ? a.row_request[row] : row;
+  const int32_t* __restrict__ bt = a.block_tables + (int64_t)request * a.bt_stride;
+  const int b0 = stage_block_ids(a, bt, pr.t_begin, pr.t_end, s_bt);
+  const int shift = a.block_shift;
+
+  // Valid heads of this workgroup: rows [0, hv) of the 16-row tiles.
+  const int hv = min(16, a.group - hg * 16);
+  const int head0 = kvh * a.group + hg * 16;
+
+  // Q^T as the B operand of S^T = K.Q^T: lane (q, c16) holds head c16's dims of
+  // chunk (4 * c + q) for k chunk c.
+  bf16x8_t qb[S::NC];
+#pragma unroll
+  for (int c = 0; c < S::NC; ++c) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (c16 < hv) v = load16(a.query + (int64_t)row * a.q_stride + (int64_t)(head0 + c16) * D + (4 * c + q) * 8);
+    qb[c] = __builtin_bit_cast(bf16x8_t, v);
+  }
+
+  f32x4_t o[S::NO];
+#pragma unroll
+  for (int c = 0; c < S::NO; ++c) o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // One buffer resource per (kv head, K or V) region of the pool: loads take
+  // 32-bit byte offsets (slot * 2D + chunk), and the range check of the
+  // resource turns any offset past the region into a zero read.
+  const uint16_t* kbase = a.pool + (int64_t)kvh * a.slots * D;
+  const uint16_t* vbase = kbase + (int64_t)a.kv_heads * a.slots * D;
+  const uint32_t region = (uint32_t)(a.slots * D * 2);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, region, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, region, kBufferDword3);
+  const int t_last = pr.t_end - 1;
+  const int block_mask = (1 << shift) - 1;
+
+  // Issue the direct loads of the step at key tb into one stage.
+  auto issue = [&](int tb, char* kt, char* vt) {
+    // K and V tiles -> LDS with 16-byte direct loads (global_load_lds_dwordx4):
+    // load i, lane l fills piece s = 64 i + l of the tile, i.e. token s / CPR,
+    // stored chunk s % CPR, which holds the token's chunk (s % CPR) ^ swz(token).
+    // One load instruction thus covers whole 128-byte lines of four keys. When
+    // the whole step lies in one pool block (block_size >= TS, the common case)
+    // its slots are consecutive and one lookup serves every key; otherwise each
+    // key is looked up, and keys past the partition read its last key (mapped,
+    // so in bounds): their scores are masked and their V rows zeroed.
+    if ((tb & block_mask) + S::TS <= block_mask + 1) {
+      const uint32_t row0 = (uint32_t)slot_of(s_bt, b0, shift, tb) * (2 * D);
+      // Load i, lane l: piece s = 64 i + l (token s / CPR, stored chunk s % CPR).
+      // The K tile is issued first, then the V tile: each a contiguous burst.
+#pragma unroll
+      for (int i = 0; i < S::LOADS; ++i) {
+        const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + i * 1024), 16,
+                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4), 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < S::LOADS; ++i) {
+        const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + i * 1024), 16,
+                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4), 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < S::LOADS; ++i) {
+        const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
+        const uint32_t row = (uint32_t)slot_of(s_bt, b0, shift, min(tb + tt, t_last)) * (2 * D);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + i * 1024), 16, row + ((pc ^ swz(tt)) << 4),
+                                                 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < S::LOADS; ++i) {
+        const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
+        const uint32_t row = (uint32_t)slot_of(s_bt, b0, shift, min(tb + tt, t_last)) * (2 * D);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + i * 1024), 16, row + ((pc ^ swz(tt)) << 4),
+                                                 0, 0, 0);
+      }
+    }
+  };
+
+  // Attend the step at key tb from one stage (its loads have landed).
+  auto consume = [&](int tb, const char* kt, char* vt) {
+    // K tile -> registers as the A operand of S^T: lane (q, c16), group h holds
+    // token 16h + c16, logical chunk 4c + q.
+    bf16x8_t kr[S::TG][S::NC];
+#pragma unroll
+    for (int h = 0; h < S::TG; ++h) {
+      const int tt = 16 * h + c16;
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c)
+        kr[h][c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt)) << 4));
+    }
+
+    // S^T = K.Q^T: lane (q, c16) gets head c16, tokens tb + 16h + 4q + r.
+    f32x4_t sc[S::TG];
+#pragma unroll
+    for (int h = 0; h < S::TG; ++h) {
+      sc[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c) sc[h] = mfma32(kr[h][c], qb[c], sc[h]);
+    }
+
+    float mx = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < S::TG; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float s;
+        if constexpr (SOFTCAP) s = a.softcap_log2 * soft_tanh(sc[h][r] * a.score_scale);
+        else s = sc[h][r] * a.score_scale;
+        s = (tb + 16 * h + 4 * q + r < pr.t_end) ? s : -INFINITY;
+        sc[h][r] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazyRescale)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+      // o rows are heads 4q + r; head h's factor lives in lanes with c16 == h.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float f = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(alpha)));
+#pragma unroll
+        for (int c = 0; c < S::NO; ++c) o[c][r] *= f;
+      }
+    }
+    const float base = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+    for (int h = 0; h < S::TG; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = fast_exp2(sc[h][r] - base);
+        sc[h][r] = p;
+        l_run += p;
+      }
+
+    // Rows of keys past the partition hold arbitrary pool data: zero them so
+    // that a zero probability cannot meet a non-finite value.
+    if (tb + S::TS > pr.t_end) {
+#pragma unroll
+      for (int i = 0; i < S::LOADS; ++i) {
+        const int s = i * 64 + lane;
+        if (tb + s / S::CPR >= pr.t_end) *reinterpret_cast<uint4*>(vt + s * 16) = make_uint4(0, 0, 0, 0);
+      }
+    }
+
+    // O[head][dim] += P . V
+    if constexpr (S::TS == 32) {
+      bf16x8_t pa;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pa[r] = (__bf16)sc[0][r];
+        pa[4 + r] = (__bf16)sc[1][r];
+      }
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) {
+        // tokens 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2); dims 16c + 4 (c16 & 3)
+        const int lc = 2 * c + ((c16 & 3) >> 1);
+        const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
+        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
+        const char* p1 = vt + t1 * (2 * D) + ((lc ^ swz(t1)) << 4) + ((c16 & 1) << 3);
+        const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)p0);
+        const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)p1);
+        const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[c] = mfma32(pa, vb, o[c]);
+      }
+    } else {
+      bf16x4_t pa;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pa[r] = (__bf16)sc[0][r];
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) {
+        const int lc = 2 * c + ((c16 & 3) >> 1);
+        const int t0 = 4 * q + (c16 >> 2);
+        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
+        const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)p0);
+        o[c] = mfma16(pa, v0, o[c]);
+      }
+    }
+    // The next step's direct loads overwrite both tiles: every read of them
+    // must have returned first.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+
+  // Two-stage pipeline: the next step's loads are in flight while the wave
+  // attends the current step; only the current stage's loads are waited for.
+  int tb = pr.t_begin;
+  issue(tb, kt0, vt0);
+  while (true) {
+    const int t1 = tb + S::TS;
+    if (t1 < pr.t_end) {
+      issue(t1, kt1, vt1);
+      wait_vmem<2 * S::LOADS>();
+    } else {
+      wait_vmem<0>();
+    }
+    consume(tb, kt0, vt0);
+    if (t1 >= pr.t_end) break;
+    const int t2 = t1 + S::TS;
+    if (t2 < pr.t_end) {
+      issue(t2, kt0, vt0);
+      wait_vmem<2 * S::LOADS>();
+    } else {
+      wait_vmem<0>();
+    }
+    consume(t1, kt1, vt1);
+    if (t2 >= pr.t_end) break;
+    tb = t2;
+  }
+
+  // Per-head sums over the four lane groups; m_run is already uniform per head.
+  l_run += shfl_xor(l_run, 16);
+  l_run += shfl_xor(l_run, 32);
+  // o rows are heads 4q + r: fetch each row's sum from lane c16 == 4q + r.
+  float lrow[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    lrow[r] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l_run)));
+
+  if (pr.nparts <= 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * q + r;
+      if (h >= hv) continue;
+      const float inv = lrow[r] > 0.f ? 1.f / lrow[r] : 0.f;
+      uint16_t* dst = a.out + (int64_t)row * a.out_stride + (int64_t)(head0 + h) * D + c16;
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(o[c][r] * inv);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * q + r;
+      if (h >= hv) continue;
+      const int64_t pi = ((int64_t)row * a.q_heads + head0 + h) * a.max_parts + blockIdx.x;
+      float* dst = a.part_o + pi * D + c16;
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) dst[16 * c] = o[c][r];
+    }
+    if (q == 0 && c16 < hv) {
+      const int64_t pi = ((int64_t)row * a.q_heads + head0 + c16) * a.max_parts + blockIdx.x;
+      a.part_ml[pi * 2] = m_run;
+      a.part_ml[pi * 2 + 1] = l_run;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dot2 kernel (small groups)
+// ---------------------------------------------------------------------------
 template <int D, int G, bool SOFTCAP>
-__global__ __launch_bounds__(kWaves * 64) void decode_partition_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kWaves * 64) void decode_dot_kernel(DecodeArgs a) {
   constexpr int LPT = D / 16;                      // lanes per token
   constexpr int TPW = 64 / LPT;                    // tokens per wave step
   constexpr int U = (D == 256) ? 4 : 32 / TPW;     // steps per iteration (even)
@@ -81,22 +448,20 @@ __global__ __launch_bounds__(kWaves * 64) void decode_partition_kernel(DecodeArg
   __shared__ float s_o[kWaves][G][D];
   __shared__ float s_m[kWaves][G];
   __shared__ float s_l[kWaves][G];
+  extern __shared__ int32_t s_bt[];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = lane / LPT, j = lane % LPT;
   const int row = blockIdx.z;
   const int kvh = blockIdx.y / a.head_groups, hg = blockIdx.y % a.head_groups;
   const int ctx = a.row_context[row];
-  const int left = visible_left(ctx, a.window);
-  const int span = ctx > left ? ctx - left : 0;
-  const int nparts = (span + a.partition - 1) / a.partition;
-  const int part = blockIdx.x;
-  if (part >= (nparts > 1 ? nparts : 1)) return;
-  const int t_begin = left + part * a.partition;
-  const int t_end = min(t_begin + a.partition, ctx);
-
+  const PartitionRange pr = partition_range(a, ctx, blockIdx.x);
+  if ((int)blockIdx.x >= (pr.nparts > 1 ? pr.nparts : 1)) return;
   const int request = a.row_request ? a.row_request[row] : row;
   const int32_t* __restrict__ bt = a.block_tables + (int64_t)request * a.bt_stride;
+  const int b0 = stage_block_ids(a, bt, pr.t_begin, pr.t_end, s_bt);
+  const int shift = a.block_shift;
+
   const int c0 = j * 8, c1 = D / 2 + j * 8;
   const int head0 = kvh * a.group + hg * G;
 
@@ -127,17 +492,16 @@ __global__ __launch_bounds__(kWaves * 64) void decode_partition_kernel(DecodeArg
 
   const uint16_t* __restrict__ kbase = a.pool + (int64_t)kvh * a.slots * D;
   const int64_t vhalf = (int64_t)a.kv_heads * a.slots * D;
-  const int bmask = (1 << a.block_shift) - 1;
 
-  for (int tb = t_begin + wave * TOK_IT; tb < t_end; tb += kWaves * TOK_IT) {
+  for (int tb = pr.t_begin + wave * TOK_IT; tb < pr.t_end; tb += kWaves * TOK_IT) {
     uint4 ka[U], kb[U], va[U], vb[U];
     bool valid[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = tb + u * TPW + grp;
-      valid[u] = t < t_end;
-      int slot = 0;
-      if (valid[u]) slot = (bt[t >> a.block_shift] << a.block_shift) | (t & bmask);
+      valid[u] = t < pr.t_end;
+      // Keys past the partition read its last key (mapped, in bounds); masked below.
+      const int slot = slot_of(s_bt, b0, shift, min(t, pr.t_end - 1));
       const uint16_t* kp = kbase + (int64_t)slot * D;
       ka[u] = load16(kp + c0);
       kb[u] = load16(kp + c1);
@@ -189,7 +553,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_partition_kernel(DecodeArg
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[gh][e] *= alpha[gh];
     }
-    if (tb + TOK_IT > t_end) {
+    if (tb + TOK_IT > pr.t_end) {
       // Tail: masked tokens read slot 0, whose contents are arbitrary; zero them
       // so that a zero probability cannot meet a non-finite value.
 #pragma unroll
@@ -260,7 +624,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_partition_kernel(DecodeArg
   }
   __syncthreads();
 
-  const bool single = nparts <= 1;
+  const bool single = pr.nparts <= 1;
   for (int idx = threadIdx.x; idx < G * D; idx += kWaves * 64) {
     const int gh = idx / D, d = idx % D;
     if (hg * G + gh >= a.group) continue;
@@ -278,7 +642,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_partition_kernel(DecodeArg
     if (single) {
       a.out[(int64_t)row * a.out_stride + (int64_t)qh * D + d] = (uint16_t)bf16_bits(ll > 0.f ? acc / ll : 0.f);
     } else {
-      const int64_t pi = ((int64_t)row * a.q_heads + qh) * a.max_parts + part;
+      const int64_t pi = ((int64_t)row * a.q_heads + qh) * a.max_parts + blockIdx.x;
       a.part_o[pi * D + d] = acc;
       if (d == 0) {
         a.part_ml[pi * 2] = mm;
@@ -288,6 +652,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_partition_kernel(DecodeArg
   }
 }
 
+// ---------------------------------------------------------------------------
+// Split-K merge
+// ---------------------------------------------------------------------------
 struct MergeArgs {
   const float* part_o;
   const float* part_ml;
@@ -349,23 +716,34 @@ void launch_merge_dispatch(int head_dim, const MergeArgs& m, hipStream_t stream)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
 template <int D, int G>
-void launch_partition(const DecodeArgs& a, bool softcap, dim3 grid, hipStream_t stream) {
-  if (softcap) decode_partition_kernel<D, G, true><<<grid, kWaves * 64, 0, stream>>>(a);
-  else decode_partition_kernel<D, G, false><<<grid, kWaves * 64, 0, stream>>>(a);
+void launch_dot(const DecodeArgs& a, bool softcap, dim3 grid, size_t lds, hipStream_t stream) {
+  if (softcap) decode_dot_kernel<D, G, true><<<grid, kWaves * 64, lds, stream>>>(a);
+  else decode_dot_kernel<D, G, false><<<grid, kWaves * 64, lds, stream>>>(a);
 }
 
 template <int D>
-void launch_partition_g(int g, const DecodeArgs& a, bool softcap, dim3 grid, hipStream_t stream) {
+void launch_dot_g(int g, const DecodeArgs& a, bool softcap, dim3 grid, size_t lds, hipStream_t stream) {
   switch (g) {
-    case 1: launch_partition<D, 1>(a, softcap, grid, stream); break;
-    case 2: launch_partition<D, 2>(a, softcap, grid, stream); break;
-    case 4: launch_partition<D, 4>(a, softcap, grid, stream); break;
-    default: launch_partition<D, 8>(a, softcap, grid, stream); break;
+    case 1: launch_dot<D, 1>(a, softcap, grid, lds, stream); break;
+    case 2: launch_dot<D, 2>(a, softcap, grid, lds, stream); break;
+    default: launch_dot<D, 3>(a, softcap, grid, lds, stream); break;
   }
 }
 
-int group_tile(int group) { return group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8; }
+template <int D>
+void launch_mfma(const DecodeArgs& a, bool softcap, dim3 grid, size_t lds, hipStream_t stream) {
+  if (softcap) decode_mfma_kernel<D, true><<<grid, 64, lds, stream>>>(a);
+  else decode_mfma_kernel<D, false><<<grid, 64, lds, stream>>>(a);
+}
+
+// Query heads one workgroup computes for a kv head: the whole group up to 16
+// (MFMA rows) when the group is >= 4, else the group itself (dot2 path).
+bool use_mfma(int group) { return group >= 4; }
+int heads_per_workgroup(int group) { return use_mfma(group) ? std::min(group, 16) : group; }
 
 int validate(const gk_decode_params* p) {
   if (!p) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: null parameters");
@@ -377,14 +755,16 @@ int validate(const gk_decode_params* p) {
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: rows, slots or max_context out of range");
   if (!is_pow2(p->block_size) || p->block_size > (1 << 20))
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: block_size must be a power of two");
-  if (p->partition_tokens < 0 || (p->partition_tokens % 32))
-    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: partition_tokens must be a multiple of 32");
+  if (p->partition_tokens < 0 || (p->partition_tokens % 32) || p->partition_tokens > 8192)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: partition_tokens must be a multiple of 32, at most 8192");
   if (!(p->scale > 0.f) || !(p->scale < INFINITY) || !(p->softcap >= 0.f) || !(p->softcap < INFINITY))
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: invalid scale or softcap");
   if (p->rows == 0) return GK_OK;
   if (!p->query || !p->pool || !p->block_tables || !p->row_context || !p->out)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: null pointer");
   const auto misaligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) != 0; };
+  if (p->slots > (int64_t)(UINT32_MAX / 2) / p->head_dim)
+    return fail(GK_ERR_UNSUPPORTED, "gk_paged_decode: one kv head's K or V region must stay below 4 GiB");
   if (misaligned(p->query) || misaligned(p->pool) || (p->q_row_stride & 7) ||
       p->q_row_stride < (int64_t)p->q_heads * p->head_dim || p->out_row_stride < (int64_t)p->q_heads * p->head_dim)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: query/pool must be 16-byte aligned with full rows");
@@ -393,11 +773,43 @@ int validate(const gk_decode_params* p) {
 
 }  // namespace
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Split-K partition (keys per work item). MFMA path: one wave per item, its
+// two K/V stages in LDS; a CU holds kLdsBytes / stage bytes of them.
+//  - Work units (row, kv head, head group) at least fill the resident waves:
+//    one item per unit (no merge), the partition covering max_context.
+//  - Otherwise 2048-key items while one round of them (at the expected mean
+//    length max_context / 2) fits the resident waves, else 1024.
+// dot2 path: halve a 2048-key partition until the items fill the GPU.
 int32_t decode_partition(const gk_decode_params* p) {
   if (p->partition_tokens > 0) return p->partition_tokens;
   const int group = p->q_heads / p->kv_heads;
-  const int64_t units = (int64_t)p->rows * p->kv_heads * ((group + group_tile(group) - 1) / group_tile(group));
+  const int hpw = heads_per_workgroup(group);
+  const int64_t units = (int64_t)p->rows * p->kv_heads * ((group + hpw - 1) / hpw);
   const int64_t mean_context = std::max<int64_t>(1, p->max_context / 2);
+  if (use_mfma(group)) {
+    constexpr int64_t kLdsBytes = 160 * 1024;
+    const int64_t stage_bytes = 2LL * 2 * (p->head_dim == 256 ? 16 : 32) * p->head_dim * 2;
+    const int64_t resident = (int64_t)device_cus() * std::max<int64_t>(1, kLdsBytes / stage_bytes);
+    if (units >= resident) {
+      int32_t part = 1024;
+      while (part < p->max_context && part < 8192) part *= 2;
+      return part;
+    }
+    return units * ((mean_context + 2047) / 2048) <= resident ? 2048 : 1024;
+  }
   int32_t part = 2048;
   while (part > 128 && units * ((mean_context + part - 1) / part) < 2048) part /= 2;
   return part;
@@ -433,7 +845,7 @@ int paged_decode(const gk_decode_params* p, void* workspace, size_t workspace_by
   if (need > workspace_bytes || (need && !workspace))
     return fail(GK_ERR_WORKSPACE, "gk_paged_decode: workspace too small (" + std::to_string(need) + " bytes needed)");
   const int group = p->q_heads / p->kv_heads;
-  const int g = group_tile(group);
+  const int hpw = heads_per_workgroup(group);
   DecodeArgs a{};
   a.query = static_cast<const uint16_t*>(p->query);
   a.q_stride = p->q_row_stride;
@@ -448,7 +860,8 @@ int paged_decode(const gk_decode_params* p, void* workspace, size_t workspace_by
   a.q_heads = p->q_heads;
   a.kv_heads = p->kv_heads;
   a.group = group;
-  a.head_groups = (group + g - 1) / g;
+  a.heads_per_group = hpw;
+  a.head_groups = (group + hpw - 1) / hpw;
   const bool softcap = p->softcap > 0.f;
   a.score_scale = softcap ? p->scale / p->softcap : p->scale * kLog2e;
   a.softcap_log2 = p->softcap * kLog2e;
@@ -463,11 +876,21 @@ int paged_decode(const gk_decode_params* p, void* workspace, size_t workspace_by
     a.part_o = static_cast<float*>(workspace);
     a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes);
   }
+  // Block-table entries one partition can span (its start need not be block aligned).
+  const size_t bt_lds = sizeof(int32_t) * (size_t)(((part - 1) >> a.block_shift) + 2);
   const dim3 grid(max_parts, p->kv_heads * a.head_groups, p->rows);
-  switch (p->head_dim) {
-    case 64: launch_partition_g<64>(g, a, softcap, grid, stream); break;
-    case 128: launch_partition_g<128>(g, a, softcap, grid, stream); break;
-    default: launch_partition_g<256>(g, a, softcap, grid, stream); break;
+  if (use_mfma(group)) {
+    switch (p->head_dim) {
+      case 64: launch_mfma<64>(a, softcap, grid, bt_lds, stream); break;
+      case 128: launch_mfma<128>(a, softcap, grid, bt_lds, stream); break;
+      default: launch_mfma<256>(a, softcap, grid, bt_lds, stream); break;
+    }
+  } else {
+    switch (p->head_dim) {
+      case 64: launch_dot_g<64>(hpw, a, softcap, grid, bt_lds, stream); break;
+      case 128: launch_dot_g<128>(hpw, a, softcap, grid, bt_lds, stream); break;
+      default: launch_dot_g<256>(hpw, a, softcap, grid, bt_lds, stream); break;
+    }
   }
   if (int rc = hip_status(hipGetLastError(), "gk_paged_decode partition launch")) return rc;
   if (max_parts > 1) {

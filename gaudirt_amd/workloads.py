@@ -10,18 +10,26 @@ import math
 import numpy as np
 
 
-def permuted_block_tables(rng, lens, block_size, num_blocks):
+def permuted_block_tables(rng, lens, block_size, num_blocks, sets=1):
+    """Seeded non-overlapping block ids: table[b, j] holds tokens [j*blk, (j+1)*blk) of sequence b.
+
+    With sets > 1, returns a list of `sets` tables over disjoint blocks of the same
+    pool (same lengths), so that consecutive benchmark steps read different memory.
+    """
     need = [(int(n) + block_size - 1) // block_size for n in lens]
     total = sum(need)
-    assert total <= num_blocks, (total, num_blocks)
-    ids = rng.permutation(num_blocks)[:total].astype(np.int32)
+    assert total * sets <= num_blocks, (total, sets, num_blocks)
+    ids = rng.permutation(num_blocks)[:total * sets].astype(np.int32)
     max_blocks = max(need)
-    table = np.full((len(lens), max_blocks), -1, dtype=np.int32)
+    tables = []
     cursor = 0
-    for b, n in enumerate(need):
-        table[b, :n] = ids[cursor:cursor + n]
-        cursor += n
-    return table
+    for _ in range(sets):
+        table = np.full((len(lens), max_blocks), -1, dtype=np.int32)
+        for b, n in enumerate(need):
+            table[b, :n] = ids[cursor:cursor + n]
+            cursor += n
+        tables.append(table)
+    return tables[0] if sets == 1 else tables
 
 
 # ---------------------------------------------------------------------------
@@ -40,7 +48,7 @@ CONFIGS = {
 class DeviceDecodeCase:
     """A decode problem whose pool and queries live on the GPU (torch tensors)."""
 
-    def __init__(self, name, seed=1234, device="cuda"):
+    def __init__(self, name, seed=1234, device="cuda", table_sets=1):
         import torch
 
         batch, heads, kv_heads, d, block, pool_blocks, sampler = CONFIGS[name]
@@ -52,10 +60,12 @@ class DeviceDecodeCase:
         self.lens = lens + 1 if self.store else lens
         need = (self.lens.astype(np.int64) + block - 1) // block
         if pool_blocks is None:
-            pool_blocks = int(need.sum())
+            pool_blocks = int(need.sum()) * table_sets
         self.batch, self.heads, self.kv_heads, self.head_dim, self.block_size = batch, heads, kv_heads, d, block
         self.scale = float(np.float32(1 / math.sqrt(d)))
-        self.tables = permuted_block_tables(rng, self.lens, block, pool_blocks)
+        tables = permuted_block_tables(rng, self.lens, block, pool_blocks, sets=table_sets)
+        self.table_sets = tables if table_sets > 1 else [tables]
+        self.tables = self.table_sets[0]
         self.slots = pool_blocks * block
         gen = torch.Generator(device=device)
         gen.manual_seed(seed)
@@ -64,12 +74,16 @@ class DeviceDecodeCase:
             for h in range(kv_heads):
                 self.pool[kind, h].normal_(generator=gen)
         self.query = torch.randn((batch, heads * d), generator=gen, device=device).to(torch.bfloat16)
-        self.d_tables = torch.from_numpy(self.tables).to(device)
+        self.d_table_sets = [torch.from_numpy(t).to(device) for t in self.table_sets]
+        self.d_tables = self.d_table_sets[0]
         self.d_lens = torch.from_numpy(self.lens).to(device)
         if self.store:
             pos = lens.astype(np.int64)
-            self.slot_mapping = (self.tables[np.arange(batch), pos // block].astype(np.int64) * block + pos % block)
-            self.d_slot_mapping = torch.from_numpy(self.slot_mapping.astype(np.int32)).to(device)
+            self.slot_mappings = [(t[np.arange(batch), pos // block].astype(np.int64) * block + pos % block)
+                                  for t in self.table_sets]
+            self.slot_mapping = self.slot_mappings[0]
+            self.d_slot_mappings = [torch.from_numpy(m.astype(np.int32)).to(device) for m in self.slot_mappings]
+            self.d_slot_mapping = self.d_slot_mappings[0]
             self.new_key = torch.randn((batch, kv_heads * d), generator=gen, device=device).to(torch.bfloat16)
             self.new_value = torch.randn((batch, kv_heads * d), generator=gen, device=device).to(torch.bfloat16)
         self.out = torch.empty((batch, heads * d), dtype=torch.bfloat16, device=device)

@@ -1,0 +1,74 @@
+"""CPU checks of the C ABI library: it loads, exports exactly what include/gaudirt_amd.h
+declares, leaves no symbol unresolved, and rejects bad arguments before any GPU work."""
+
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+from gaudirt_amd import capi
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "gaudirt_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(gk_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not capi.LIB_PATH.exists():
+        pytest.fail(f"{capi.LIB_PATH} is not built: run `python -m gaudirt_amd.build`")
+    return capi.load()
+
+
+def test_header_declarations_are_exported(lib):
+    names = declared_functions()
+    assert "gk_paged_decode" in names and "gk_kv_store" in names
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    # The Python binding lists the same set.
+    assert set(capi.EXPORTED) == names, set(capi.EXPORTED) ^ names
+
+
+def test_no_unresolved_symbols():
+    # A kernel whose host stub was not instantiated shows up as an undefined
+    # symbol only when the library is loaded on a GPU box; catch it here.
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(capi.LIB_PATH)], check=True,
+                         capture_output=True, text=True).stdout
+    unresolved = [line.split()[-1] for line in out.splitlines()
+                  if line.split() and line.split()[0] == "U" and "@" not in line.split()[-1]]
+    assert not unresolved, unresolved
+
+
+def test_version_and_error_convention(lib):
+    assert lib.gk_version().decode().startswith("gaudirt_amd")
+    rc = lib.gk_paged_decode(None, None, 0, None)
+    assert rc == capi.GK_ERR_INVALID_ARGUMENT
+    assert "null parameters" in lib.gk_last_error().decode()
+
+
+def test_decode_validation_rejects_before_launch(lib):
+    p = capi.DecodeParams()
+    p.rows, p.q_heads, p.kv_heads, p.head_dim = 4, 8, 2, 96
+    p.block_size, p.slots, p.scale = 128, 8192, 0.1
+    assert lib.gk_paged_decode(ctypes.byref(p), None, 0, None) == capi.GK_ERR_UNSUPPORTED
+    assert "head dimension" in lib.gk_last_error().decode()
+    p.head_dim, p.block_size = 128, 96
+    assert lib.gk_paged_decode(ctypes.byref(p), None, 0, None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "power of two" in lib.gk_last_error().decode()
+    p.block_size, p.q_heads = 128, 7
+    assert lib.gk_paged_decode(ctypes.byref(p), None, 0, None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "head geometry" in lib.gk_last_error().decode()
+
+
+def test_kv_store_validation(lib):
+    rc = lib.gk_kv_store(None, None, 128, 128, None, 4, None, 64, 1, 100, None)
+    assert rc == capi.GK_ERR_INVALID_ARGUMENT and "geometry" in lib.gk_last_error().decode()
+    assert lib.gk_kv_store(None, None, 128, 128, None, 0, None, 64, 1, 128, None) == capi.GK_OK
