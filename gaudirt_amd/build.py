@@ -75,7 +75,8 @@ def build_extension():
                "-DUSE_ROCM=1", "-D__HIP_PLATFORM_AMD__=1"]
     src = CSRC / "torch_ext.cpp"
     obj = BUILD / "torch_ext.o"
-    _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-I", str(ROOT / "include"), "-I", str(CSRC), "-I", py_include,
+    _run([HIPCC, "-O2", "-std=c++20", "-fPIC", f"--offload-arch={ARCH}", "-I", str(ROOT / "include"), "-I", str(CSRC),
+          "-I", py_include,
           *includes, *defines, "-c", str(src), "-o", str(obj), "-Wno-unused-result"])
     lib_dirs = cpp_extension.library_paths()
     suffix = sysconfig.get_config_var("EXT_SUFFIX")
@@ -93,7 +94,8 @@ def build_extension():
 
 def build(jobs=8):
     lib = build_library(jobs)
-    return (lib,)
+    ext = build_extension()
+    return lib, ext
 
 
 if __name__ == "__main__":

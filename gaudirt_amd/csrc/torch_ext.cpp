@@ -1,0 +1,559 @@
+// PyTorch-ROCm binding of the paged-attention path: the reference's operator
+// API for it (TORCH_LIBRARY gaudirt, src/bridge/generic_private_use1.cpp:430-489),
+// with every device step going through the C ABI of libgaudirt_amd.so.
+//
+//   torch.classes.gaudirt.PagedMetadata   slot mapping, block tables, lengths
+//   torch.ops.gaudirt.paged_attn          KV store + attention over the pool
+//   torch.ops.gaudirt._paged_attn_validated
+//   torch.ops.gaudirt._advance_decode_lengths
+//   gaudirt_amd._C._allocate_paged_kv     head-major pool on the block allocator
+//
+// Errors are TORCH_CHECK failures (RuntimeError in Python) raised before any
+// KV byte is written, with the message fragments the reference's tests match.
+#include <ATen/ATen.h>
+#include <c10/core/Storage.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/custom_class.h>
+#include <torch/extension.h>
+#include <torch/library.h>
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <bit>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "gaudirt_amd.h"
+
+namespace gaudirt_amd {
+namespace {
+
+void check_gk(int rc, const char* what) {
+  TORCH_CHECK(rc == GK_OK, what, ": ", gk_last_error());
+}
+
+hipStream_t current_stream() { return c10::hip::getCurrentHIPStream().stream(); }
+
+int current_device() {
+  int dev = 0;
+  TORCH_CHECK(hipGetDevice(&dev) == hipSuccess, "GaudiRT: no current HIP device");
+  return dev;
+}
+
+at::TensorOptions device_int32() {
+  return at::TensorOptions().device(at::Device(at::kCUDA, current_device())).dtype(at::kInt);
+}
+
+// ---------------------------------------------------------------------------
+// Stream-ordered block allocator behind the KV pools (one per device).
+// ---------------------------------------------------------------------------
+std::mutex g_alloc_mutex;
+std::array<gk_allocator*, 64> g_allocators{};
+
+gk_allocator* device_allocator(int device) {
+  TORCH_CHECK(device >= 0 && device < 64, "GaudiRT: invalid device index ", device);
+  std::lock_guard<std::mutex> lock(g_alloc_mutex);
+  if (!g_allocators[device]) {
+    size_t free_bytes = 0, total_bytes = 0;
+    c10::hip::HIPGuard guard(device);
+    TORCH_CHECK(hipMemGetInfo(&free_bytes, &total_bytes) == hipSuccess, "GaudiRT: hipMemGetInfo failed");
+    gk_allocator* a = nullptr;
+    check_gk(gk_allocator_create(device, total_bytes, 256ull << 20, &a), "GaudiRT: KV allocator");
+    g_allocators[device] = a;
+  }
+  return g_allocators[device];
+}
+
+struct PoolBlock {
+  gk_allocator* allocator;
+  void* base;
+};
+
+void free_pool_block(void* ctx) {
+  auto* block = static_cast<PoolBlock*>(ctx);
+  (void)gk_allocator_free(block->allocator, block->base);
+  delete block;
+}
+
+// If `tensor` lives in a pool from the block allocator, record `stream` as a
+// user so the block is fenced before any reuse on another stream.
+void record_pool_stream(const at::Tensor& tensor, hipStream_t stream) {
+  const auto& dp = tensor.storage().data_ptr();
+  if (dp.get_deleter() != &free_pool_block) return;
+  auto* block = static_cast<PoolBlock*>(dp.get_context());
+  check_gk(gk_allocator_record_stream(block->allocator, block->base, stream), "GaudiRT: KV pool record_stream");
+}
+
+// allocate_paged_kv (src/bridge/paged_kv_pool.cpp:15-41): zeroed bf16
+// [layers, 2, kv_heads, slots, head_dim]; layer l's key pool view is
+// pool[l, 0].transpose(0, 1) -> [slots, kv_heads, head_dim], its value pool
+// pool[l, 1].transpose(0, 1). The reference's 131072-slot descriptor cap is a
+// Synapse artefact and is not kept; one head's K (or V) region must stay below
+// 4 GiB (32-bit buffer offsets).
+at::Tensor allocate_paged_kv(int64_t layers, int64_t slots, int64_t heads, int64_t head_dim) {
+  TORCH_CHECK(layers > 0 && layers <= 4096 && slots > 0 && heads > 0 && heads <= 256 &&
+                  (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+                  slots <= static_cast<int64_t>(std::numeric_limits<uint32_t>::max() / 2) / head_dim,
+              "GaudiRT: unsupported head-major KV pool geometry");
+  const uint64_t layer_bytes = 2ull * heads * slots * head_dim * sizeof(uint16_t);
+  TORCH_CHECK(layer_bytes <= std::numeric_limits<uint64_t>::max() / static_cast<uint64_t>(layers),
+              "GaudiRT: KV pool size overflow");
+  const uint64_t bytes = layer_bytes * layers;
+  const int device = current_device();
+  gk_allocator* allocator = device_allocator(device);
+  const hipStream_t stream = current_stream();
+  void* base = nullptr;
+  check_gk(gk_allocator_alloc(allocator, bytes, stream, &base), "GaudiRT: KV pool allocation");
+  auto* block = new PoolBlock{allocator, base};
+  c10::DataPtr data(base, block, &free_pool_block, at::Device(at::kCUDA, device));
+  c10::Storage storage(c10::Storage::use_byte_size_t(), bytes, std::move(data), nullptr, false);
+  auto pool = at::empty({0}, at::TensorOptions().device(at::kCUDA, device).dtype(at::kBFloat16));
+  pool.set_(storage, 0, {layers, 2, heads, slots, head_dim},
+            {2 * heads * slots * head_dim, heads * slots * head_dim, slots * head_dim, head_dim, 1});
+  TORCH_CHECK(hipMemsetAsync(base, 0, bytes, stream) == hipSuccess, "GaudiRT: failed to initialize KV pool");
+  return pool;
+}
+
+pybind11::dict allocator_stats(int64_t device) {
+  gk_allocator_stats s{};
+  check_gk(gk_allocator_get_stats(device_allocator(static_cast<int>(device)), &s), "GaudiRT: allocator stats");
+  pybind11::dict d;
+  d["allocated_bytes"] = s.allocated_bytes;
+  d["peak_bytes"] = s.peak_bytes;
+  d["reserved_bytes"] = s.reserved_bytes;
+  d["largest_free_block"] = s.largest_free_block;
+  d["slabs"] = s.slabs;
+  d["events_created"] = s.events_created;
+  return d;
+}
+
+// ---------------------------------------------------------------------------
+// Attention plan: a device int32 tensor [row_request | row_context | block
+// tables] whose DataPtr context owns the host-side schedule, so launches need
+// no device-to-host read (the reference keeps its AttentionPlan the same way,
+// src/bridge/attention_plan.cpp:31-34,132-140).
+// ---------------------------------------------------------------------------
+struct PlanInfo {
+  int64_t rows = 0, query_heads = 0, kv_heads = 0, head_dim = 0, slots = 0;
+  int64_t block_size = 1, bt_stride = 0, requests = 0, max_context = 0, sliding_window = -1;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  at::Tensor storage;  // the plan's own device buffer
+  int64_t row_request_offset = 0, row_context_offset = 0, block_table_offset = 0;
+};
+
+void release_plan(void* ctx) { delete static_cast<PlanInfo*>(ctx); }
+
+at::Tensor make_plan_tensor(std::unique_ptr<PlanInfo> info) {
+  const auto& buffer = info->storage;
+  const auto nbytes = buffer.nbytes();
+  const auto numel = buffer.numel();
+  void* data = buffer.data_ptr();
+  const auto device = buffer.device();
+  c10::DataPtr dp(data, info.release(), &release_plan, device);
+  c10::Storage storage(c10::Storage::use_byte_size_t(), nbytes, std::move(dp), nullptr, false);
+  auto plan = at::empty({0}, at::TensorOptions().device(device).dtype(at::kInt));
+  plan.set_(storage, 0, {numel}, {1});
+  return plan;
+}
+
+const PlanInfo& plan_data(const at::Tensor& tensor) {
+  TORCH_CHECK(tensor.is_cuda() && tensor.device().index() == current_device(),
+              "GaudiRT attention: expected a device metadata plan");
+  const auto& dp = tensor.storage().data_ptr();
+  TORCH_CHECK(dp.get_deleter() == &release_plan && tensor.data_ptr() == dp.get(),
+              "GaudiRT attention: invalid or expired metadata plan");
+  return *static_cast<const PlanInfo*>(dp.get_context());
+}
+
+// ---------------------------------------------------------------------------
+// PagedMetadata (src/bridge/paged_metadata.hpp:17-109, host constructor
+// src/bridge/paged_metadata.cpp:82-174).
+// ---------------------------------------------------------------------------
+class PagedMetadata : public torch::CustomClassHolder {
+ public:
+  static constexpr int64_t kMaxRows = 8192;
+
+  PagedMetadata(const at::Tensor& locations, const at::Tensor& requests, const at::Tensor& positions,
+                const at::Tensor& mapping, int64_t slots) {
+    for (const auto& tensor : {locations, requests, positions, mapping})
+      TORCH_CHECK(tensor.device().is_cpu() && tensor.is_contiguous() &&
+                      (tensor.scalar_type() == at::kInt || tensor.scalar_type() == at::kLong),
+                  "GaudiRT: paged metadata must be contiguous CPU int32 or int64");
+    TORCH_CHECK(locations.dim() == 1 && requests.dim() == 1 && positions.dim() == 1 && mapping.dim() == 2 &&
+                    locations.size(0) == requests.size(0) && locations.size(0) == positions.size(0),
+                "GaudiRT: invalid paged metadata ranks or row counts");
+    const int64_t m = locations.size(0), request_count = mapping.size(0), context = mapping.size(1);
+    TORCH_CHECK(m > 0 && m <= kMaxRows && slots > 0 && slots <= std::numeric_limits<int32_t>::max() &&
+                    request_count > 0 && request_count <= std::numeric_limits<int32_t>::max() && context > 0 &&
+                    context <= std::numeric_limits<int32_t>::max() &&
+                    mapping.numel() <= std::numeric_limits<int32_t>::max(),
+                "GaudiRT: paged metadata dimensions outside supported range");
+    const auto read = [](const at::Tensor& t, int64_t i) -> int64_t {
+      return t.scalar_type() == at::kInt ? t.data_ptr<int32_t>()[i] : t.data_ptr<int64_t>()[i];
+    };
+    mapping_h_.resize(mapping.numel());
+    for (int64_t i = 0; i < mapping.numel(); ++i) {
+      const auto slot = read(mapping, i);
+      TORCH_CHECK(slot >= -1 && slot < slots, "GaudiRT: request-to-token slot is out of range");
+      mapping_h_[i] = static_cast<int32_t>(slot);
+    }
+    locations_h_.resize(m);
+    requests_h_.resize(m);
+    positions_h_.resize(m);
+    max_position_.assign(request_count, -1);
+    std::unordered_map<int32_t, std::pair<int32_t, int32_t>> targets;
+    targets.reserve(m * 2);
+    for (int64_t i = 0; i < m; ++i) {
+      const auto slot = read(locations, i), request = read(requests, i), position = read(positions, i);
+      TORCH_CHECK(slot >= 0 && slot < slots && request >= 0 && request < request_count && position >= 0 &&
+                      position < context,
+                  "GaudiRT: paged metadata index is out of range");
+      TORCH_CHECK(mapping_h_[request * context + position] == slot,
+                  "GaudiRT: output slot does not match request-to-token mapping");
+      const bool inserted =
+          targets.emplace(static_cast<int32_t>(slot), std::make_pair(static_cast<int32_t>(request),
+                                                                     static_cast<int32_t>(position)))
+              .second;
+      TORCH_CHECK(inserted, "GaudiRT: duplicate output KV slot");
+      locations_h_[i] = static_cast<int32_t>(slot);
+      requests_h_[i] = static_cast<int32_t>(request);
+      positions_h_[i] = static_cast<int32_t>(position);
+      if (i == 0 || requests_h_[i - 1] != request || positions_h_[i - 1] + 1 != position)
+        sequences_.push_back({static_cast<int32_t>(i), 1, static_cast<int32_t>(position)});
+      else
+        ++sequences_.back().length;
+      max_position_[request] = std::max(max_position_[request], static_cast<int32_t>(position));
+    }
+    for (int64_t request = 0; request < request_count; ++request) {
+      for (int32_t position = 0; position <= max_position_[request]; ++position) {
+        const auto slot = mapping_h_[request * context + position];
+        TORCH_CHECK(slot >= 0, "GaudiRT: missing KV slot in a visible prefix");
+        auto target = targets.find(slot);
+        TORCH_CHECK(target == targets.end() ||
+                        (target->second.first == request && target->second.second == position),
+                    "GaudiRT: output KV slot aliases another visible prefix position");
+      }
+    }
+    rows_ = m;
+    slots_ = slots;
+    request_count_ = request_count;
+    context_ = context;
+    // Device copies for the kernels and for the row accessors.
+    const auto upload = [&](const std::vector<int32_t>& v, std::vector<int64_t> shape) {
+      auto host = at::from_blob(const_cast<int32_t*>(v.data()), shape, at::TensorOptions().dtype(at::kInt));
+      return host.to(device_int32().device(), /*non_blocking=*/false, /*copy=*/true);
+    };
+    locations_ = upload(locations_h_, {m});
+    requests_ = upload(requests_h_, {m});
+    positions_ = upload(positions_h_, {m});
+    mapping_ = upload(mapping_h_, {request_count, context});
+    const std::vector<int32_t> header{static_cast<int32_t>(m)};
+    header_ = upload(header, {1});
+  }
+
+  int64_t rows() const { return rows_; }
+  int64_t slots() const { return slots_; }
+  int64_t context() const { return context_; }
+  at::Tensor rotary_positions() const { return positions_; }
+  at::Tensor rotary_header() const { return header_; }
+  at::Tensor row_locations() const { return locations_; }
+  at::Tensor row_requests() const { return requests_; }
+  at::Tensor request_mapping() const { return mapping_; }
+  at::Tensor model_positions() const {
+    TORCH_CHECK(false, "GaudiRT: model positions require fused scheduler metadata");
+    return {};
+  }
+  at::Tensor last_token_indices() const {
+    TORCH_CHECK(false, "GaudiRT: last-token indices require batched metadata");
+    return {};
+  }
+  at::Tensor token_ids() const {
+    TORCH_CHECK(false, "GaudiRT: token IDs were not validated in this metadata");
+    return {};
+  }
+  int64_t vocabulary() const { return 0; }
+  std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, int64_t>
+  forward_tensors(int64_t query_heads, int64_t kv_heads, int64_t head_dim) {
+    return {token_ids(), last_token_indices(), rotary_positions(), rotary_header(), row_locations(),
+            row_requests(), attention_plan(query_heads, kv_heads, head_dim), context_};
+  }
+
+  at::Tensor attention_plan(int64_t query_heads, int64_t kv_heads, int64_t head_dim) {
+    return attention_plan_for(query_heads, kv_heads, head_dim, -1);
+  }
+
+  // attention_plan_for (src/bridge/attention_plan.cpp:146-172 for the checks).
+  at::Tensor attention_plan_for(int64_t query_heads, int64_t kv_heads, int64_t head_dim, int64_t sliding_window) {
+    TORCH_CHECK(sliding_window == -1 || (sliding_window > 0 && sliding_window <= std::numeric_limits<int32_t>::max()),
+                "GaudiRT attention: invalid sliding window size");
+    const int64_t window = sliding_window > 0 ? sliding_window : -1;
+    auto cached = plans_.find(window);
+    if (cached != plans_.end()) {
+      const auto& plan = plan_data(cached->second);
+      TORCH_CHECK(plan.query_heads == query_heads && plan.kv_heads == kv_heads && plan.head_dim == head_dim,
+                  "GaudiRT attention: metadata already bound to different head geometry");
+      return cached->second;
+    }
+    TORCH_CHECK(query_heads > 0 && query_heads <= 1024 && kv_heads > 0 && kv_heads <= 256 &&
+                    query_heads % kv_heads == 0 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+                    slots_ > 0 && slots_ <= static_cast<int64_t>(std::numeric_limits<uint32_t>::max() / 2) / head_dim,
+                "GaudiRT attention: unsupported head or request-map geometry");
+    auto info = std::make_unique<PlanInfo>();
+    info->rows = rows_;
+    info->query_heads = query_heads;
+    info->kv_heads = kv_heads;
+    info->head_dim = head_dim;
+    info->slots = slots_;
+    info->requests = request_count_;
+    info->sliding_window = window;
+    info->device = current_device();
+    info->stream = current_stream();
+    // Block tables: the largest power-of-two page P (<= 1024) for which every
+    // visible token t of every request sits at mapping[r, t - t % P] + t % P
+    // with a P-aligned page start; P = 1 keeps the token-granular map.
+    const int64_t page = page_size();
+    const int64_t max_pages = std::max<int64_t>(1, (context_ + page - 1) / page);
+    std::vector<int32_t> tables(request_count_ * max_pages, -1);
+    for (int64_t r = 0; r < request_count_; ++r)
+      for (int64_t t = 0; t <= max_position_[r]; t += page)
+        tables[r * max_pages + t / page] = mapping_h_[r * context_ + t] / static_cast<int32_t>(page);
+    std::vector<int32_t> words;
+    words.reserve(2 * rows_ + tables.size());
+    info->row_request_offset = 0;
+    words.insert(words.end(), requests_h_.begin(), requests_h_.end());
+    info->row_context_offset = rows_;
+    int64_t max_context = 0;
+    for (int64_t i = 0; i < rows_; ++i) {
+      words.push_back(positions_h_[i] + 1);
+      max_context = std::max<int64_t>(max_context, positions_h_[i] + 1);
+    }
+    // keep the block tables 16-byte aligned
+    while (words.size() % 4) words.push_back(0);
+    info->block_table_offset = static_cast<int64_t>(words.size());
+    words.insert(words.end(), tables.begin(), tables.end());
+    info->block_size = page;
+    info->bt_stride = max_pages;
+    info->max_context = max_context;
+    auto host = at::from_blob(words.data(), {static_cast<int64_t>(words.size())}, at::TensorOptions().dtype(at::kInt));
+    info->storage = host.to(device_int32().device(), false, true);
+    auto plan = make_plan_tensor(std::move(info));
+    plans_.emplace(window, plan);
+    return plan;
+  }
+
+ private:
+  struct Sequence {
+    int32_t row, length, prefix;
+  };
+
+  int64_t page_size() const {
+    for (int64_t page = 1024; page > 1; page >>= 1) {
+      bool ok = true;
+      for (int64_t r = 0; r < request_count_ && ok; ++r) {
+        const int32_t* map = mapping_h_.data() + r * context_;
+        for (int64_t t = 0; t <= max_position_[r] && ok; ++t) {
+          const int64_t start = t - t % page;
+          ok = map[start] % page == 0 && map[t] == map[start] + t % page;
+        }
+      }
+      if (ok) return page;
+    }
+    return 1;
+  }
+
+  int64_t rows_ = 0, slots_ = 0, request_count_ = 0, context_ = 0;
+  std::vector<int32_t> locations_h_, requests_h_, positions_h_, mapping_h_, max_position_;
+  std::vector<Sequence> sequences_;
+  at::Tensor locations_, requests_, positions_, mapping_, header_;
+  std::unordered_map<int64_t, at::Tensor> plans_;
+};
+
+// Output storage of pow2(rows) rows rounded to 256 bytes, shaped [rows, width]
+// (bucket_output, src/bridge/generic_private_use1.cpp:207-219).
+at::Tensor bucket_output(const at::Tensor& like, int64_t rows, int64_t width) {
+  const uint64_t bucket = std::bit_ceil(static_cast<uint64_t>(rows));
+  const uint64_t bytes = (bucket * width * sizeof(uint16_t) + 255) & ~uint64_t{255};
+  auto output = at::empty({static_cast<int64_t>(bytes / sizeof(uint16_t))}, like.options().dtype(at::kBFloat16));
+  output.unsafeGetTensorImpl()->set_sizes_contiguous({rows, width});
+  return output;
+}
+
+// Rows of a 2-D bf16 matrix as the kernels take them: 16-byte aligned, row
+// stride a multiple of 8 elements, unit column stride; else a packed copy.
+at::Tensor kernel_rows(const at::Tensor& t) {
+  const bool ok = t.stride(1) == 1 && t.stride(0) % 8 == 0 && t.stride(0) >= t.size(1) &&
+                  (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0;
+  return ok ? t : t.contiguous();
+}
+
+// paged_attn_validated / paged_attn_internal (src/bridge/paged_attention.cpp:164-347):
+// store the rows' K/V into the pool, then attend every row over its request's
+// visible keys.
+at::Tensor paged_attn_validated(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
+                                const at::Tensor& key_pool, const at::Tensor& value_pool, const at::Tensor& locations,
+                                const at::Tensor& requests, const at::Tensor& positions, const at::Tensor& plan_tensor,
+                                const at::Tensor& header, int64_t head_dim, double scale, double softcap,
+                                int64_t sliding_window) {
+  (void)requests;
+  (void)positions;
+  (void)header;
+  const auto& plan = plan_data(plan_tensor);
+  const hipStream_t stream = current_stream();
+  const float scale_f = static_cast<float>(scale), softcap_f = static_cast<float>(softcap);
+  TORCH_CHECK(plan.stream == stream && std::isfinite(scale) && std::isfinite(scale_f) && scale_f > 0 &&
+                  std::isfinite(softcap) && std::isfinite(softcap_f) && softcap_f >= 0.0f &&
+                  (sliding_window == -1 || (sliding_window > 0 && sliding_window <= std::numeric_limits<int32_t>::max())) &&
+                  head_dim == plan.head_dim,
+              "GaudiRT attention: invalid scale, stream, or head dimension");
+  TORCH_CHECK(plan.sliding_window <= 0 || plan.sliding_window == sliding_window,
+              "GaudiRT attention: plan sliding_window mismatch");
+  const int device = current_device();
+  for (const auto& input : {query, key, value})
+    TORCH_CHECK(input.is_cuda() && input.device().index() == device && input.scalar_type() == at::kBFloat16 &&
+                    input.dim() == 2 && input.size(0) == plan.rows,
+                "GaudiRT attention: Q/K/V must be BF16 device matrices with matching rows");
+  TORCH_CHECK(query.size(1) == plan.query_heads * head_dim && key.size(1) == plan.kv_heads * head_dim &&
+                  value.size(1) == key.size(1) && locations.dim() == 1 && locations.numel() == plan.rows &&
+                  locations.scalar_type() == at::kInt && locations.is_cuda(),
+              "GaudiRT attention: Q/K/V or slot dimensions do not match metadata");
+  for (const auto& pool : {key_pool, value_pool})
+    TORCH_CHECK(pool.is_cuda() && pool.device().index() == device && pool.scalar_type() == at::kBFloat16 &&
+                    pool.dim() == 3 && pool.size(0) == plan.slots && pool.size(1) == plan.kv_heads &&
+                    pool.size(2) == head_dim && pool.stride(0) == head_dim && pool.stride(1) == plan.slots * head_dim &&
+                    pool.stride(2) == 1,
+                "GaudiRT attention: head-major combined KV pool is required");
+  const auto pool_address = reinterpret_cast<uintptr_t>(key_pool.data_ptr());
+  const auto value_address = reinterpret_cast<uintptr_t>(value_pool.data_ptr());
+  const uint64_t value_offset = static_cast<uint64_t>(plan.slots) * plan.kv_heads * head_dim * sizeof(uint16_t);
+  const auto& pool_storage = key_pool.storage();
+  const auto storage_base = reinterpret_cast<uintptr_t>(pool_storage.data());
+  TORCH_CHECK(pool_storage.unsafeGetStorageImpl() == value_pool.storage().unsafeGetStorageImpl() &&
+                  value_address == pool_address + value_offset && pool_address >= storage_base &&
+                  pool_address % 256 == 0 &&
+                  pool_address - storage_base + 2 * value_offset <= pool_storage.nbytes(),
+              "GaudiRT attention: KV pool descriptor is not backed by combined storage");
+  record_pool_stream(key_pool, stream);
+
+  const auto q = kernel_rows(query), k = kernel_rows(key), v = kernel_rows(value);
+  auto output = bucket_output(query, plan.rows, query.size(1));
+  void* pool = key_pool.data_ptr();
+  // KV store first, on the same stream: rows of one sequence attend each
+  // other's new keys.
+  check_gk(gk_kv_store(k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), locations.data_ptr<int32_t>(),
+                       static_cast<int32_t>(plan.rows), pool, plan.slots, static_cast<int32_t>(plan.kv_heads),
+                       static_cast<int32_t>(head_dim), stream),
+           "GaudiRT attention: KV store");
+  const int32_t* words = plan.storage.data_ptr<int32_t>();
+  gk_decode_params p{};
+  p.query = q.data_ptr();
+  p.q_row_stride = q.stride(0);
+  p.pool = pool;
+  p.slots = plan.slots;
+  p.block_tables = words + plan.block_table_offset;
+  p.bt_stride = plan.bt_stride;
+  p.block_size = static_cast<int32_t>(plan.block_size);
+  p.row_request = words + plan.row_request_offset;
+  p.row_context = words + plan.row_context_offset;
+  p.rows = static_cast<int32_t>(plan.rows);
+  p.q_heads = static_cast<int32_t>(plan.query_heads);
+  p.kv_heads = static_cast<int32_t>(plan.kv_heads);
+  p.head_dim = static_cast<int32_t>(head_dim);
+  p.scale = scale_f;
+  p.softcap = softcap_f;
+  p.sliding_window = sliding_window > 0 ? static_cast<int32_t>(sliding_window) : -1;
+  p.max_context = static_cast<int32_t>(plan.max_context);
+  p.out = output.data_ptr();
+  p.out_row_stride = output.stride(0);
+  const size_t need = gk_paged_decode_workspace_bytes(&p);
+  at::Tensor workspace;
+  if (need) workspace = at::empty({static_cast<int64_t>(need)}, query.options().dtype(at::kByte));
+  check_gk(gk_paged_decode(&p, need ? workspace.data_ptr() : nullptr, need, stream), "GaudiRT attention");
+  return output;
+}
+
+// paged_attn (src/bridge/generic_private_use1.cpp:277-293).
+at::Tensor paged_attn(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
+                      const at::Tensor& key_pool, const at::Tensor& value_pool,
+                      const c10::intrusive_ptr<PagedMetadata>& metadata, int64_t head_dim, double scale, double softcap,
+                      int64_t sliding_window) {
+  TORCH_CHECK(metadata, "GaudiRT paged attention: metadata is required");
+  TORCH_CHECK(query.dim() == 2 && key_pool.dim() == 3 && (head_dim == 64 || head_dim == 128 || head_dim == 256),
+              "GaudiRT paged attention: invalid tensor ranks or head dimension");
+  const auto q_heads = query.size(1) / head_dim;
+  const auto kv_heads = key_pool.size(1);
+  auto plan = sliding_window > 0 ? metadata->attention_plan_for(q_heads, kv_heads, head_dim, sliding_window)
+                                 : metadata->attention_plan(q_heads, kv_heads, head_dim);
+  return paged_attn_validated(query, key, value, key_pool, value_pool, metadata->row_locations(),
+                              metadata->row_requests(), metadata->rotary_positions(), plan, metadata->rotary_header(),
+                              head_dim, scale, softcap, sliding_window);
+}
+
+// advance_decode_lengths (src/bridge/eager_scheduler.cpp:50-82).
+std::tuple<at::Tensor, at::Tensor> advance_decode_lengths(const at::Tensor& seq_lens, const at::Tensor& orig_seq_lens) {
+  TORCH_CHECK(seq_lens.is_cuda() && orig_seq_lens.device() == seq_lens.device() &&
+                  seq_lens.scalar_type() == at::kLong && orig_seq_lens.scalar_type() == at::kInt &&
+                  seq_lens.dim() == 1 && orig_seq_lens.sizes() == seq_lens.sizes() &&
+                  seq_lens.numel() <= std::numeric_limits<int>::max() && seq_lens.is_contiguous() &&
+                  orig_seq_lens.is_contiguous(),
+              "GaudiRT decode lengths: expected matching contiguous int64 and int32 vectors");
+  auto next = at::empty_like(seq_lens), orig_next = at::empty_like(orig_seq_lens);
+  if (!seq_lens.numel()) return {next, orig_next};
+  TORCH_CHECK(seq_lens.numel() <= (1LL << 30), "GaudiRT decode lengths: count exceeds supported range");
+  check_gk(gk_advance_decode_lengths(seq_lens.data_ptr<int64_t>(), orig_seq_lens.data_ptr<int32_t>(), seq_lens.numel(),
+                                     next.data_ptr<int64_t>(), orig_next.data_ptr<int32_t>(), current_stream()),
+           "GaudiRT decode lengths");
+  return {next, orig_next};
+}
+
+}  // namespace
+}  // namespace gaudirt_amd
+
+TORCH_LIBRARY(gaudirt, m) {
+  using gaudirt_amd::PagedMetadata;
+  m.class_<PagedMetadata>("PagedMetadata")
+      .def(torch::init<at::Tensor, at::Tensor, at::Tensor, at::Tensor, int64_t>())
+      .def("rows", &PagedMetadata::rows)
+      .def("slots", &PagedMetadata::slots)
+      .def("context", &PagedMetadata::context)
+      .def("forward_tensors", &PagedMetadata::forward_tensors)
+      .def("rotary_positions", &PagedMetadata::rotary_positions)
+      .def("model_positions", &PagedMetadata::model_positions)
+      .def("rotary_header", &PagedMetadata::rotary_header)
+      .def("row_locations", &PagedMetadata::row_locations)
+      .def("row_requests", &PagedMetadata::row_requests)
+      .def("request_mapping", &PagedMetadata::request_mapping)
+      .def("attention_plan", &PagedMetadata::attention_plan)
+      .def("attention_plan_for", &PagedMetadata::attention_plan_for)
+      .def("last_token_indices", &PagedMetadata::last_token_indices)
+      .def("token_ids", &PagedMetadata::token_ids)
+      .def("vocabulary", &PagedMetadata::vocabulary);
+  m.def("paged_attn(Tensor query, Tensor key, Tensor value, Tensor(a!) key_pool, Tensor(b!) value_pool, "
+        "__torch__.torch.classes.gaudirt.PagedMetadata metadata, int head_dim, float scale, "
+        "float softcap=0.0, int sliding_window=-1) -> Tensor");
+  m.def("_paged_attn_validated(Tensor query, Tensor key, Tensor value, Tensor(a!) key_pool, Tensor(b!) value_pool, "
+        "Tensor locations, Tensor requests, Tensor positions, Tensor mapping, Tensor header, "
+        "int head_dim, float scale, float softcap=0.0, int sliding_window=-1) -> Tensor");
+  m.def("_advance_decode_lengths(Tensor seq_lens, Tensor orig_seq_lens) -> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(gaudirt, CUDA, m) {
+  m.impl("paged_attn", TORCH_FN(gaudirt_amd::paged_attn));
+  m.impl("_paged_attn_validated", TORCH_FN(gaudirt_amd::paged_attn_validated));
+  m.impl("_advance_decode_lengths", TORCH_FN(gaudirt_amd::advance_decode_lengths));
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("_allocate_paged_kv", &gaudirt_amd::allocate_paged_kv, "zeroed head-major bf16 KV pool");
+  m.def("_kv_allocator_stats", &gaudirt_amd::allocator_stats, pybind11::arg("device") = 0);
+  m.def("_paged_attn_kv_tile", [](int64_t) { return 512; });
+  m.def("version", []() { return std::string(gk_version()); });
+}

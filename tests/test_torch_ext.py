@@ -1,0 +1,126 @@
+"""CPU checks of the torch boundary: exact schemas, PagedMetadata validation
+messages (raised before any device work), fake kernels, and the KV-tile query.
+
+Message fragments follow the reference's host constructor
+(src/bridge/paged_metadata.cpp:82-140) and the tests that match them
+(tests/paged_metadata_smoke.py:38-54 of the reference).
+"""
+
+import pytest
+import torch
+
+import gaudirt_amd
+
+SCHEMAS = {
+    "paged_attn": "gaudirt::paged_attn(Tensor query, Tensor key, Tensor value, Tensor(a!) key_pool, "
+                  "Tensor(b!) value_pool, __torch__.torch.classes.gaudirt.PagedMetadata metadata, int head_dim, "
+                  "float scale, float softcap=0.0, int sliding_window=-1) -> Tensor",
+    "_paged_attn_validated": "gaudirt::_paged_attn_validated(Tensor query, Tensor key, Tensor value, "
+                             "Tensor(a!) key_pool, Tensor(b!) value_pool, Tensor locations, Tensor requests, "
+                             "Tensor positions, Tensor mapping, Tensor header, int head_dim, float scale, "
+                             "float softcap=0.0, int sliding_window=-1) -> Tensor",
+    "_advance_decode_lengths": "gaudirt::_advance_decode_lengths(Tensor seq_lens, Tensor orig_seq_lens) "
+                               "-> (Tensor, Tensor)",
+}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def ext():
+    return gaudirt_amd.load_extension()
+
+
+@pytest.mark.parametrize("name", sorted(SCHEMAS))
+def test_schema_strings(name):
+    # Registered from the reference's exact strings; compared after parsing, as
+    # torch prints defaults in its own normal form (0.0 -> 0.).
+    assert getattr(torch.ops.gaudirt, name).default._schema == torch._C.parse_schema(SCHEMAS[name])
+
+
+def test_paged_metadata_methods_exist():
+    # TorchScript resolves every method of the class with its signature; a
+    # missing or mistyped method fails compilation.
+    @torch.jit.script
+    def uses_all(m: torch.classes.gaudirt.PagedMetadata, w: int):
+        sizes = m.rows() + m.slots() + m.context() + m.vocabulary()
+        rows = (m.rotary_positions(), m.rotary_header(), m.row_locations(), m.row_requests(),
+                m.request_mapping(), m.model_positions(), m.last_token_indices(), m.token_ids())
+        plans = (m.attention_plan(32, 8, 128), m.attention_plan_for(32, 8, 128, w))
+        return sizes, rows, plans, m.forward_tensors(32, 8, 128)
+
+    assert uses_all is not None
+
+
+def _meta(locations, requests, positions, mapping, slots):
+    return torch.classes.gaudirt.PagedMetadata(locations, requests, positions, mapping, slots)
+
+
+def _base():
+    mapping = torch.arange(16, dtype=torch.int32).reshape(2, 8)
+    requests = torch.tensor([0, 1], dtype=torch.int64)
+    positions = torch.tensor([2, 3], dtype=torch.int64)
+    locations = mapping[requests, positions].to(torch.int64)
+    return locations, requests, positions, mapping
+
+
+@pytest.mark.parametrize("case,fragment", [
+    ("float", "contiguous CPU int32 or int64"),
+    ("rank", "invalid paged metadata ranks"),
+    ("rows", "dimensions outside supported range"),
+    ("map_range", "request-to-token slot is out of range"),
+    ("index", "index is out of range"),
+    ("mismatch", "does not match"),
+    ("duplicate", "duplicate output KV slot"),
+    ("missing", "missing KV slot"),
+    ("alias", "aliases another visible prefix"),
+])
+def test_metadata_rejections(case, fragment):
+    locations, requests, positions, mapping = _base()
+    slots = 16
+    if case == "float":
+        locations = locations.float()
+    elif case == "rank":
+        requests = requests[:1]
+    elif case == "rows":
+        locations = torch.zeros(8193, dtype=torch.int64)
+        requests = torch.zeros(8193, dtype=torch.int64)
+        positions = torch.zeros(8193, dtype=torch.int64)
+    elif case == "map_range":
+        mapping = mapping.clone()
+        mapping[0, 7] = 16
+    elif case == "index":
+        positions = positions.clone()
+        positions[1] = 8
+    elif case == "mismatch":
+        locations = locations.clone()
+        locations[0] = 5
+    elif case == "duplicate":
+        mapping = mapping.clone()
+        mapping[1, 3] = int(mapping[0, 2])
+        locations = torch.tensor([2, 2], dtype=torch.int64)
+    elif case == "missing":
+        mapping = mapping.clone()
+        mapping[0, 1] = -1
+    elif case == "alias":
+        # request 1's visible prefix contains the slot request 0 is writing
+        mapping = mapping.clone()
+        mapping[1, 0] = int(mapping[0, 2])
+    with pytest.raises(RuntimeError, match=fragment):
+        _meta(locations, requests, positions, mapping, slots)
+
+
+def test_fake_kernels_on_meta_tensors():
+    q = torch.empty(5, 8 * 64, device="meta", dtype=torch.bfloat16)
+    k = torch.empty(5, 2 * 64, device="meta", dtype=torch.bfloat16)
+    pool = torch.empty(32, 2, 64, device="meta", dtype=torch.bfloat16)
+    idx = torch.empty(5, device="meta", dtype=torch.int32)
+    out = torch.ops.gaudirt._paged_attn_validated(q, k, k, pool, pool, idx, idx, idx, idx, idx, 64, 0.125)
+    assert out.shape == q.shape and out.device.type == "meta"
+    seq = torch.empty(7, device="meta", dtype=torch.int64)
+    orig = torch.empty(7, device="meta", dtype=torch.int32)
+    a, b = torch.ops.gaudirt._advance_decode_lengths(seq, orig)
+    assert a.shape == seq.shape and b.dtype == torch.int32
+
+
+def test_kv_tile_and_version(ext):
+    assert gaudirt_amd.paged_attn_kv_tile(1) == 512
+    assert ext.version().startswith("gaudirt_amd")
