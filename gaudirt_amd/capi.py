@@ -24,7 +24,7 @@ GK_ERR_WORKSPACE = 5
 # Every function include/gaudirt_amd.h declares.
 EXPORTED = [
     "gk_last_error", "gk_version", "gk_kv_store", "gk_paged_decode_workspace_bytes",
-    "gk_paged_decode_partition_tokens", "gk_paged_decode", "gk_split_k_merge",
+    "gk_paged_decode_partition_tokens", "gk_paged_decode", "gk_paged_prefill", "gk_split_k_merge",
     "gk_attn_tile_indices", "gk_advance_decode_lengths",
     "gk_allocator_create", "gk_allocator_destroy", "gk_allocator_alloc", "gk_allocator_record_stream",
     "gk_allocator_free", "gk_allocator_empty_cache", "gk_allocator_get_stats",
@@ -36,8 +36,17 @@ c_i64 = ctypes.c_int64
 c_f32 = ctypes.c_float
 
 
-class DecodeParams(ctypes.Structure):
+class _Sized(ctypes.Structure):
+    """Parameter struct whose leading struct_size field is filled in on construction."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.struct_size = ctypes.sizeof(self)
+
+
+class DecodeParams(_Sized):
     _fields_ = [
+        ("struct_size", ctypes.c_size_t),
         ("query", c_void_p), ("q_row_stride", c_i64),
         ("pool", c_void_p), ("slots", c_i64),
         ("block_tables", c_void_p), ("bt_stride", c_i64), ("block_size", c_i32),
@@ -47,7 +56,21 @@ class DecodeParams(ctypes.Structure):
         ("max_context", c_i32), ("partition_tokens", c_i32),
         ("out", c_void_p), ("out_row_stride", c_i64),
         ("new_key", c_void_p), ("new_value", c_void_p), ("new_kv_row_stride", c_i64),
-        ("slot_mapping", c_void_p),
+        ("slot_mapping", c_void_p), ("row_map", c_void_p),
+    ]
+
+
+class PrefillParams(_Sized):
+    _fields_ = [
+        ("struct_size", ctypes.c_size_t),
+        ("query", c_void_p), ("q_row_stride", c_i64),
+        ("pool", c_void_p), ("slots", c_i64),
+        ("block_tables", c_void_p), ("bt_stride", c_i64), ("block_size", c_i32),
+        ("seq_request", c_void_p), ("seq_first_row", c_void_p), ("seq_rows", c_void_p), ("seq_prefix", c_void_p),
+        ("seqs", c_i32), ("max_rows", c_i32),
+        ("q_heads", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32),
+        ("scale", c_f32), ("softcap", c_f32), ("sliding_window", c_i32),
+        ("out", c_void_p), ("out_row_stride", c_i64),
     ]
 
 
@@ -80,6 +103,7 @@ def load():
     lib.gk_paged_decode_partition_tokens.restype = c_i32
     lib.gk_paged_decode_partition_tokens.argtypes = [ctypes.POINTER(DecodeParams)]
     lib.gk_paged_decode.argtypes = [ctypes.POINTER(DecodeParams), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.gk_paged_prefill.argtypes = [ctypes.POINTER(PrefillParams), c_void_p]
     lib.gk_kv_store.argtypes = [c_void_p, c_void_p, c_i64, c_i64, c_void_p, c_i32, c_void_p, c_i64, c_i32, c_i32,
                                 c_void_p]
     lib.gk_split_k_merge.argtypes = [c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_i32, c_i32, c_void_p, c_i64,

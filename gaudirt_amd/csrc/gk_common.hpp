@@ -99,5 +99,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 int launch_kv_store(const void* key, const void* value, int64_t key_stride, int64_t value_stride,
                     const int32_t* slot_mapping, int32_t rows, void* pool, int64_t slots, int32_t kv_heads,
                     int32_t head_dim, hipStream_t stream);
+int paged_prefill(const gk_prefill_params* params, hipStream_t stream);
 
 }  // namespace gk

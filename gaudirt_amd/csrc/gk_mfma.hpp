@@ -1,0 +1,64 @@
+// Device building blocks shared by the gfx950 attention kernels: bf16 MFMA
+// tiles, buffer resources, the LDS token swizzle and the transposed LDS read.
+#pragma once
+
+#include "gk_common.hpp"
+
+namespace gk {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Word 3 of a raw buffer resource on gfx950 (32-bit data format, offset mode).
+constexpr int kBufferDword3 = 0x00020000;
+
+__device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// tanh via exp2: tanh(x) = 1 - 2 / (2^(2x log2 e) + 1); saturates cleanly at +-1.
+__device__ __forceinline__ float soft_tanh(float x) {
+  const float e = fast_exp2(2.f * kLog2e * x);
+  return 1.f - 2.f / (e + 1.f);
+}
+
+// Pool slot of key t from block ids staged in LDS: s_bt[i] is the block id of
+// block b0 + i (block size 2^shift).
+__device__ __forceinline__ int slot_of(const int32_t* s_bt, int b0, int shift, int t) {
+  return (s_bt[(t >> shift) - b0] << shift) | (t & ((1 << shift) - 1));
+}
+
+// Token swizzle of 16-byte chunks inside an LDS row of a K or V tile: chunk c
+// of token t is stored at c ^ swz(t). Conflict-free both for the row-major
+// tile writes and for the 16-key operand reads (8 consecutive tokens map to 8
+// distinct chunk slots) and the transposed 4-token reads of P.V (4 consecutive
+// tokens map to distinct 32-byte pairs).
+__device__ __forceinline__ int swz(int t) { return ((t & 3) << 1) | ((t >> 2) & 1); }
+
+// Wait until at most N vector memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// D += A . B on 16x16 tiles, K = 32 (8 bf16 per lane) or K = 16 (4 per lane).
+// Lane (q = lane / 16, c = lane % 16): A row c and B column c, k slots of group
+// q; D rows 4q .. 4q + 3, column c.
+__device__ __forceinline__ f32x4_t mfma32(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma16(const bf16x4_t& a, const bf16x4_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, a), __builtin_bit_cast(i16x4_t, b), c,
+                                                   0, 0, 0);
+}
+
+// Four consecutive LDS rows (16-bit elements), transposed: lane i of each
+// 16-lane group receives column i of the 4 x 16 block its group addresses
+// (lane j addresses row j / 4, columns 4 (j % 4) .. + 3).
+__device__ __forceinline__ bf16x4_t lds_read_tr4(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)p);
+}
+
+}  // namespace gk

@@ -35,7 +35,7 @@
 // q.k times scale; probabilities are rounded to bf16 before P.V as in the
 // reference, but relative to a running rather than the final max, and
 // normalised once at the end; sums use the unrounded fp32 probabilities.
-#include "gk_common.hpp"
+#include "gk_mfma.hpp"
 
 #include <algorithm>
 
@@ -64,6 +64,7 @@ struct DecodeArgs {
   int32_t block_shift;
   const int32_t* row_request;
   const int32_t* row_context;
+  const int32_t* row_map;
   int32_t rows, q_heads, kv_heads, group, head_groups, heads_per_group;
   float score_scale;  // scale * log2(e), or scale / softcap when capping
   float softcap_log2; // softcap * log2(e) when capping
@@ -74,16 +75,8 @@ struct DecodeArgs {
   float* part_ml;
 };
 
-__device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-
 __device__ __forceinline__ uint32_t word(const uint4& v, int e) {
   return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
-}
-
-// tanh via exp2: tanh(x) = 1 - 2 / (2^(2x log2 e) + 1); saturates cleanly at +-1.
-__device__ __forceinline__ float soft_tanh(float x) {
-  const float e = fast_exp2(2.f * kLog2e * x);
-  return 1.f - 2.f / (e + 1.f);
 }
 
 __device__ __forceinline__ int visible_left(int ctx, int window) {
@@ -116,22 +109,9 @@ __device__ __forceinline__ int stage_block_ids(const DecodeArgs& a, const int32_
   return b0;
 }
 
-__device__ __forceinline__ int slot_of(const int32_t* s_bt, int b0, int shift, int t) {
-  return (s_bt[(t >> shift) - b0] << shift) | (t & ((1 << shift) - 1));
-}
-
 // ---------------------------------------------------------------------------
 // MFMA kernel
 // ---------------------------------------------------------------------------
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
-typedef __attribute__((address_space(3))) void lds_void_t;
-// Word 3 of a raw buffer resource on gfx950 (32-bit data format, offset mode).
-constexpr int kBufferDword3 = 0x00020000;
-
 template <int D>
 struct MfmaShape {
   static constexpr int TS = D == 256 ? 16 : 32;   // keys per step
@@ -142,25 +122,6 @@ struct MfmaShape {
   static constexpr int NO = D / 16;               // 16-dim output chunks of P.V
   static constexpr int TILE = TS * D * 2;         // bytes of one K or V tile in LDS
 };
-
-// Token swizzle of 16-byte chunks inside an LDS row: chunk c of token t is
-// stored at c ^ swz(t). Conflict-free both for the row-major tile writes and
-// for the transposed 4-token reads of P.V.
-__device__ __forceinline__ int swz(int t) { return ((t & 3) << 1) | ((t >> 2) & 1); }
-
-// Wait until at most N vector memory operations of this wave are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ f32x4_t mfma32(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x4_t mfma16(const bf16x4_t& a, const bf16x4_t& b, const f32x4_t& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, a), __builtin_bit_cast(i16x4_t, b), c,
-                                                   0, 0, 0);
-}
 
 // One wave per workgroup; the workgroup owns (partition blockIdx.x, kv head /
 // head group blockIdx.y, query row blockIdx.z). Waves never synchronise with
@@ -181,6 +142,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
   const int lane = threadIdx.x;
   const int q = lane >> 4, c16 = lane & 15;
   const int row = blockIdx.z;
+  const int qrow = a.row_map ? a.row_map[row] : row;  // query/output row of this work row
   const int kvh = blockIdx.y / a.head_groups, hg = blockIdx.y % a.head_groups;
   const int ctx = a.row_context[row];
   const PartitionRange pr = partition_range(a, ctx, blockIdx.x);
@@ -200,7 +162,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
 #pragma unroll
   for (int c = 0; c < S::NC; ++c) {
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (c16 < hv) v = load16(a.query + (int64_t)row * a.q_stride + (int64_t)(head0 + c16) * D + (4 * c + q) * 8);
+    if (c16 < hv) v = load16(a.query + (int64_t)qrow * a.q_stride + (int64_t)(head0 + c16) * D + (4 * c + q) * 8);
     qb[c] = __builtin_bit_cast(bf16x8_t, v);
   }
 
@@ -348,8 +310,8 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
         const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
         const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
         const char* p1 = vt + t1 * (2 * D) + ((lc ^ swz(t1)) << 4) + ((c16 & 1) << 3);
-        const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)p0);
-        const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)p1);
+        const bf16x4_t v0 = lds_read_tr4(p0);
+        const bf16x4_t v1 = lds_read_tr4(p1);
         const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
         o[c] = mfma32(pa, vb, o[c]);
       }
@@ -362,7 +324,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
         const int lc = 2 * c + ((c16 & 3) >> 1);
         const int t0 = 4 * q + (c16 >> 2);
         const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
-        const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)p0);
+        const bf16x4_t v0 = lds_read_tr4(p0);
         o[c] = mfma16(pa, v0, o[c]);
       }
     }
@@ -412,7 +374,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
       const int h = 4 * q + r;
       if (h >= hv) continue;
       const float inv = lrow[r] > 0.f ? 1.f / lrow[r] : 0.f;
-      uint16_t* dst = a.out + (int64_t)row * a.out_stride + (int64_t)(head0 + h) * D + c16;
+      uint16_t* dst = a.out + (int64_t)qrow * a.out_stride + (int64_t)(head0 + h) * D + c16;
 #pragma unroll
       for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(o[c][r] * inv);
     }
@@ -453,6 +415,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_dot_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = lane / LPT, j = lane % LPT;
   const int row = blockIdx.z;
+  const int qrow = a.row_map ? a.row_map[row] : row;  // query/output row of this work row
   const int kvh = blockIdx.y / a.head_groups, hg = blockIdx.y % a.head_groups;
   const int ctx = a.row_context[row];
   const PartitionRange pr = partition_range(a, ctx, blockIdx.x);
@@ -470,7 +433,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_dot_kernel(DecodeArgs a) {
   for (int gh = 0; gh < G; ++gh) {
     uint4 x = make_uint4(0, 0, 0, 0), y = make_uint4(0, 0, 0, 0);
     if (hg * G + gh < a.group) {
-      const uint16_t* q = a.query + (int64_t)row * a.q_stride + (int64_t)(head0 + gh) * D;
+      const uint16_t* q = a.query + (int64_t)qrow * a.q_stride + (int64_t)(head0 + gh) * D;
       x = load16(q + c0);
       y = load16(q + c1);
     }
@@ -640,7 +603,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_dot_kernel(DecodeArgs a) {
     }
     const int qh = head0 + gh;
     if (single) {
-      a.out[(int64_t)row * a.out_stride + (int64_t)qh * D + d] = (uint16_t)bf16_bits(ll > 0.f ? acc / ll : 0.f);
+      a.out[(int64_t)qrow * a.out_stride + (int64_t)qh * D + d] = (uint16_t)bf16_bits(ll > 0.f ? acc / ll : 0.f);
     } else {
       const int64_t pi = ((int64_t)row * a.q_heads + qh) * a.max_parts + blockIdx.x;
       a.part_o[pi * D + d] = acc;
@@ -660,6 +623,7 @@ struct MergeArgs {
   const float* part_ml;
   const int32_t* part_count;   // explicit counts, or
   const int32_t* row_context;  // derive counts from contexts when part_count is null
+  const int32_t* row_map;      // output row of each work row (null = identity)
   int32_t window, partition;
   int32_t rows, heads, max_parts;
   uint16_t* out;
@@ -698,7 +662,8 @@ __global__ __launch_bounds__(64) void split_k_merge_kernel(MergeArgs a) {
     for (int k = 0; k < PER_LANE; ++k) acc[k] += sc * a.part_o[(base + p) * D + lane + 64 * k];
   }
   const float inv = ll > 0.f ? 1.f / ll : 0.f;
-  uint16_t* dst = a.out + (int64_t)row * a.out_stride + (int64_t)head * D;
+  const int orow = a.row_map ? a.row_map[row] : row;
+  uint16_t* dst = a.out + (int64_t)orow * a.out_stride + (int64_t)head * D;
 #pragma unroll
   for (int k = 0; k < PER_LANE; ++k) dst[lane + 64 * k] = (uint16_t)bf16_bits(acc[k] * inv);
 }
@@ -747,6 +712,8 @@ int heads_per_workgroup(int group) { return use_mfma(group) ? std::min(group, 16
 
 int validate(const gk_decode_params* p) {
   if (!p) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: null parameters");
+  if (p->struct_size != sizeof(gk_decode_params))
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode: struct_size does not match this library's gk_decode_params");
   if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256)
     return fail(GK_ERR_UNSUPPORTED, "gk_paged_decode: head dimension must be 64, 128 or 256");
   if (p->q_heads <= 0 || p->kv_heads <= 0 || p->q_heads % p->kv_heads || p->q_heads > 1024)
@@ -856,6 +823,7 @@ int paged_decode(const gk_decode_params* p, void* workspace, size_t workspace_by
   a.block_shift = log2_int(p->block_size);
   a.row_request = p->row_request;
   a.row_context = p->row_context;
+  a.row_map = p->row_map;
   a.rows = p->rows;
   a.q_heads = p->q_heads;
   a.kv_heads = p->kv_heads;
@@ -898,6 +866,7 @@ int paged_decode(const gk_decode_params* p, void* workspace, size_t workspace_by
     m.part_o = a.part_o;
     m.part_ml = a.part_ml;
     m.row_context = p->row_context;
+    m.row_map = p->row_map;
     m.window = a.window;
     m.partition = part;
     m.rows = p->rows;
@@ -938,11 +907,11 @@ int split_k_merge(const float* partial_out, const float* partial_ml, const int32
 }  // namespace gk
 
 extern "C" size_t gk_paged_decode_workspace_bytes(const gk_decode_params* params) {
-  return params ? gk::decode_workspace_bytes(params) : 0;
+  return params && params->struct_size == sizeof(gk_decode_params) ? gk::decode_workspace_bytes(params) : 0;
 }
 
 extern "C" int32_t gk_paged_decode_partition_tokens(const gk_decode_params* params) {
-  return params ? gk::decode_partition(params) : 0;
+  return params && params->struct_size == sizeof(gk_decode_params) ? gk::decode_partition(params) : 0;
 }
 
 extern "C" int gk_paged_decode(const gk_decode_params* params, void* workspace, size_t workspace_bytes,

@@ -1,0 +1,347 @@
+// Chunked / prefix-shared paged prefill attention for gfx950 (bf16 MFMA).
+//
+// A sequence contributes a chunk of consecutive query rows at positions
+// prefix .. prefix + rows - 1; row i attends keys [left_i, prefix + i] of its
+// request (causal; left_i = prefix + i - window + 1 with a sliding window).
+// The chunk's own K/V rows are already in the pool (the store runs first), so
+// every key is read through the block table.
+//
+// Work decomposition. A workgroup of four waves owns one (sequence, kv head,
+// tile of rows). The GQA group is folded into the tile: its 128 "query rows"
+// are (row, head) pairs, so one K/V tile serves every head of the group. Each
+// wave computes 32 query rows (two 16-column MFMA tiles) against 32 keys per
+// step:
+//   S^T[key][qrow] = K . Q^T      v_mfma_f32_16x16x32_bf16, K from LDS
+//   O[qrow][dim]  += P . V        P straight from S^T's registers, V read
+//                                 transposed from LDS (ds_read_b64_tr_b16)
+// K and V tiles of 32 keys are shared by the four waves through LDS: 16-byte
+// buffer->LDS loads issued by the whole workgroup, XOR-swizzled by token,
+// double-buffered so the next tile streams in while the current one is used.
+// Online softmax runs in log2 units with a lazily re-based running maximum.
+//
+// Numerics versus the reference (the tile chain of
+// src/bridge/paged_attention_tiles.cpp:87-225): fp32 scores times scale,
+// probabilities rounded to bf16 before P.V (relative to the running maximum),
+// fp32 accumulation, one normalisation at the end, bf16 output.
+#include "gk_mfma.hpp"
+
+#include <algorithm>
+
+namespace gk {
+namespace {
+
+constexpr int kPrefillWaves = 4;
+constexpr int kQrowsPerWave = 32;                          // two 16-column tiles
+constexpr int kQrows = kPrefillWaves * kQrowsPerWave;     // query rows per workgroup
+constexpr int kKeys = 32;                                  // keys per step
+constexpr float kLazyRescale = 8.f;
+
+struct PrefillArgs {
+  const uint16_t* query;
+  int64_t q_stride;
+  const uint16_t* pool;
+  int64_t slots;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  int32_t block_shift;
+  const int32_t* seq_request;
+  const int32_t* seq_first_row;
+  const int32_t* seq_rows;
+  const int32_t* seq_prefix;
+  int32_t q_heads, kv_heads, group, rows_per_tile;
+  float score_scale;   // scale * log2(e), or scale / softcap when capping
+  float softcap_log2;  // softcap * log2(e) when capping
+  int32_t window;
+  uint16_t* out;
+  int64_t out_stride;
+};
+
+template <int D>
+struct PrefillShape {
+  static constexpr int NC = D / 32;                 // 32-dim k chunks of Q.K
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per head row
+  static constexpr int NO = D / 16;                 // 16-dim output chunks
+  static constexpr int TILE = kKeys * D * 2;        // bytes of one K or V tile
+  static constexpr int LOADS = TILE / (kPrefillWaves * 64 * 16);  // per thread per tile
+};
+
+template <int D, bool SOFTCAP>
+__global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillArgs a) {
+  using S = PrefillShape<D>;
+  __shared__ __attribute__((aligned(16))) char kt0[S::TILE];
+  __shared__ __attribute__((aligned(16))) char vt0[S::TILE];
+  __shared__ __attribute__((aligned(16))) char kt1[S::TILE];
+  __shared__ __attribute__((aligned(16))) char vt1[S::TILE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, c16 = lane & 15;
+  const int seq = blockIdx.z, kvh = blockIdx.y;
+  const int rows = a.seq_rows[seq];
+  const int r0 = blockIdx.x * a.rows_per_tile;
+  if (r0 >= rows) return;
+  const int nr = min(a.rows_per_tile, rows - r0);
+  const int prefix = a.seq_prefix[seq];
+  const int first_row = a.seq_first_row[seq] + r0;
+  const int32_t* __restrict__ bt = a.block_tables + (int64_t)a.seq_request[seq] * a.bt_stride;
+  const int g = a.group;
+  const int pos_lo = prefix + r0, pos_hi = prefix + r0 + nr - 1;
+  const int key_end = pos_hi + 1;
+  const int key_begin = a.window > 0 ? max(0, pos_lo - a.window + 1) : 0;
+  const int kb0 = key_begin & ~(kKeys - 1);
+  const int nsteps = (key_end - kb0 + kKeys - 1) / kKeys;
+
+  // This lane's two query rows (one per 16-column tile): qrow = (row, head).
+  int qpos[2], qleft[2];
+  bool qvalid[2];
+  bf16x8_t qb[2][S::NC];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int qr = wave * kQrowsPerWave + nt * 16 + c16;
+    const int row = qr / g, head = qr % g;
+    qvalid[nt] = row < nr;
+    qpos[nt] = qvalid[nt] ? pos_lo + row : -1;
+    qleft[nt] = a.window > 0 ? qpos[nt] - a.window + 1 : 0;
+    const uint16_t* src = a.query + (int64_t)(first_row + row) * a.q_stride + (int64_t)(kvh * g + head) * D;
+#pragma unroll
+    for (int c = 0; c < S::NC; ++c) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (qvalid[nt]) v = load16(src + (4 * c + q) * 8);
+      qb[nt][c] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+
+  f32x4_t o[2][S::NO];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int c = 0; c < S::NO; ++c) o[nt][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+
+  const uint16_t* kbase = a.pool + (int64_t)kvh * a.slots * D;
+  const uint16_t* vbase = kbase + (int64_t)a.kv_heads * a.slots * D;
+  const uint32_t region = (uint32_t)(a.slots * D * 2);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, region, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, region, kBufferDword3);
+  const int shift = a.block_shift, bmask = (1 << shift) - 1;
+
+  // Direct loads of the 32-key step at tb into one stage. Steps are 32-aligned
+  // and blocks hold >= 32 keys, so a step lies in one block: its slots are
+  // consecutive from the block's slot for tb (one scalar block-table read).
+  // Piece p = 64 (LOADS * wave + i) + lane: token p / CPR, stored chunk
+  // p % CPR holding the token's chunk (p % CPR) ^ swz(token).
+  auto issue = [&](int tb, char* kt, char* vt) {
+    const uint32_t row0 = (uint32_t)((bt[tb >> shift] << shift) | (tb & bmask)) * (2 * D);
+#pragma unroll
+    for (int i = 0; i < S::LOADS; ++i) {
+      const int p = (S::LOADS * wave + i) * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + (S::LOADS * wave + i) * 1024), 16,
+                                               row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4), 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < S::LOADS; ++i) {
+      const int p = (S::LOADS * wave + i) * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + (S::LOADS * wave + i) * 1024), 16,
+                                               row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4), 0, 0, 0);
+    }
+  };
+
+  auto consume = [&](int tb, const char* kt, char* vt) {
+    if (tb + kKeys > key_end) {
+      // Keys past the tile's last row hold arbitrary pool data: zero their V
+      // rows so that a zero probability cannot meet a non-finite value.
+      for (int p = tid; p < kKeys * S::CPR; p += kPrefillWaves * 64)
+        if (tb + p / S::CPR >= key_end) *reinterpret_cast<uint4*>(vt + p * 16) = make_uint4(0, 0, 0, 0);
+      __syncthreads();
+    }
+    // S^T = K.Q^T: lane (q, c16) gets qrow c16 (+16 nt), keys tb + 16h + 4q + r.
+    f32x4_t sc[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int tt = 16 * h + c16;
+      bf16x8_t kr[S::NC];
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c)
+        kr[c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt)) << 4));
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        sc[h][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < S::NC; ++c) sc[h][nt] = mfma32(kr[c], qb[nt][c], sc[h][nt]);
+      }
+    }
+
+    bf16x8_t pa[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = tb + 16 * h + 4 * q + r;
+          float s;
+          if constexpr (SOFTCAP) s = a.softcap_log2 * soft_tanh(sc[h][nt][r] * a.score_scale);
+          else s = sc[h][nt][r] * a.score_scale;
+          s = (key <= qpos[nt] && key >= qleft[nt]) ? s : -INFINITY;
+          sc[h][nt][r] = s;
+          mx = fmaxf(mx, s);
+        }
+      mx = fmaxf(mx, shfl_xor(mx, 16));
+      mx = fmaxf(mx, shfl_xor(mx, 32));
+      if (__builtin_amdgcn_ballot_w64(mx > m_run[nt] + kLazyRescale)) {
+        const float m_new = fmaxf(m_run[nt], mx);
+        const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
+        l_run[nt] *= alpha;
+        m_run[nt] = m_new;
+        // o rows are qrows 4q + r; qrow h's factor lives in lanes with c16 == h.
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float f = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(alpha)));
+#pragma unroll
+          for (int c = 0; c < S::NO; ++c) o[nt][c][r] *= f;
+        }
+      }
+      const float base = m_run[nt] == -INFINITY ? 0.f : m_run[nt];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = fast_exp2(sc[h][nt][r] - base);
+          l_run[nt] += p;
+          pa[nt][4 * h + r] = (__bf16)p;
+        }
+    }
+
+    // O[qrow][dim] += P . V: keys 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2),
+    // dims 16c + 4 (c16 & 3), read transposed.
+#pragma unroll
+    for (int c = 0; c < S::NO; ++c) {
+      const int lc = 2 * c + ((c16 & 3) >> 1);
+      const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
+      const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3));
+      const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1)) << 4) + ((c16 & 1) << 3));
+      const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) o[nt][c] = mfma32(pa[nt], vb, o[nt][c]);
+    }
+  };
+
+  // Two-stage pipeline over the workgroup: the next tile's loads are in flight
+  // while the current one is attended. Barriers: (1) every wave's loads of the
+  // current stage have landed, (2) every wave is done with a stage before it
+  // is refilled.
+  int tb = kb0;
+  issue(tb, kt0, vt0);
+  for (int step = 0; step < nsteps; step += 2) {
+    const bool more1 = step + 1 < nsteps;
+    if (more1) {
+      issue(tb + kKeys, kt1, vt1);
+      wait_vmem<2 * S::LOADS>();
+    } else {
+      wait_vmem<0>();
+    }
+    __syncthreads();
+    consume(tb, kt0, vt0);
+    __syncthreads();
+    if (!more1) break;
+    const bool more2 = step + 2 < nsteps;
+    if (more2) {
+      issue(tb + 2 * kKeys, kt0, vt0);
+      wait_vmem<2 * S::LOADS>();
+    } else {
+      wait_vmem<0>();
+    }
+    __syncthreads();
+    consume(tb + kKeys, kt1, vt1);
+    __syncthreads();
+    tb += 2 * kKeys;
+  }
+
+  // Per-qrow sums over the four lane groups, then normalise and store.
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    float l = l_run[nt];
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      // o row 4q + r of tile nt; its sum lives in lane c16 == 4q + r.
+      const float lr = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l)));
+      const int qr = wave * kQrowsPerWave + nt * 16 + 4 * q + r;
+      const int row = qr / g, head = qr % g;
+      if (row >= nr) continue;
+      const float inv = lr > 0.f ? 1.f / lr : 0.f;
+      uint16_t* dst = a.out + (int64_t)(first_row + row) * a.out_stride + (int64_t)(kvh * g + head) * D + c16;
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(o[nt][c][r] * inv);
+    }
+  }
+}
+
+template <int D>
+void launch(const PrefillArgs& a, bool softcap, dim3 grid, hipStream_t stream) {
+  if (softcap) prefill_kernel<D, true><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+  else prefill_kernel<D, false><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+}
+
+}  // namespace
+
+int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
+  if (!p) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: null parameters");
+  if (p->struct_size != sizeof(gk_prefill_params))
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: struct_size does not match this library's gk_prefill_params");
+  if (p->head_dim != 64 && p->head_dim != 128)
+    return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: head dimension must be 64 or 128");
+  if (p->q_heads <= 0 || p->kv_heads <= 0 || p->q_heads % p->kv_heads || p->q_heads / p->kv_heads > kQrows)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: invalid head geometry (GQA group at most 128)");
+  if (!is_pow2(p->block_size) || p->block_size < kKeys || p->block_size > (1 << 20))
+    return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: block_size must be a power of two of at least 32");
+  if (p->seqs < 0 || p->seqs > 65535 || p->max_rows < 0 || p->slots <= 0)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: sequence count, rows or slots out of range");
+  if (p->slots > (int64_t)(UINT32_MAX / 2) / p->head_dim)
+    return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: one kv head's K or V region must stay below 4 GiB");
+  if (!(p->scale > 0.f) || !(p->scale < INFINITY) || !(p->softcap >= 0.f) || !(p->softcap < INFINITY))
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: invalid scale or softcap");
+  if (p->seqs == 0 || p->max_rows == 0) return GK_OK;
+  if (!p->query || !p->pool || !p->block_tables || !p->seq_request || !p->seq_first_row || !p->seq_rows ||
+      !p->seq_prefix || !p->out)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: null pointer");
+  const auto misaligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) != 0; };
+  if (misaligned(p->query) || misaligned(p->pool) || (p->q_row_stride & 7) ||
+      p->q_row_stride < (int64_t)p->q_heads * p->head_dim || p->out_row_stride < (int64_t)p->q_heads * p->head_dim)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: query/pool must be 16-byte aligned with full rows");
+  PrefillArgs a{};
+  a.query = static_cast<const uint16_t*>(p->query);
+  a.q_stride = p->q_row_stride;
+  a.pool = static_cast<const uint16_t*>(p->pool);
+  a.slots = p->slots;
+  a.block_tables = p->block_tables;
+  a.bt_stride = p->bt_stride;
+  a.block_shift = log2_int(p->block_size);
+  a.seq_request = p->seq_request;
+  a.seq_first_row = p->seq_first_row;
+  a.seq_rows = p->seq_rows;
+  a.seq_prefix = p->seq_prefix;
+  a.q_heads = p->q_heads;
+  a.kv_heads = p->kv_heads;
+  a.group = p->q_heads / p->kv_heads;
+  a.rows_per_tile = kQrows / a.group;
+  const bool softcap = p->softcap > 0.f;
+  a.score_scale = softcap ? p->scale / p->softcap : p->scale * kLog2e;
+  a.softcap_log2 = p->softcap * kLog2e;
+  a.window = p->sliding_window > 0 ? p->sliding_window : 0;
+  a.out = static_cast<uint16_t*>(p->out);
+  a.out_stride = p->out_row_stride;
+  const dim3 grid((p->max_rows + a.rows_per_tile - 1) / a.rows_per_tile, p->kv_heads, p->seqs);
+  if (grid.x > 65535u * 1024u) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: too many rows");
+  if (p->head_dim == 64) launch<64>(a, softcap, grid, stream);
+  else launch<128>(a, softcap, grid, stream);
+  return hip_status(hipGetLastError(), "gk_paged_prefill launch");
+}
+
+}  // namespace gk
+
+extern "C" int gk_paged_prefill(const gk_prefill_params* params, hipStream_t stream) {
+  gk::clear_error();
+  return gk::paged_prefill(params, stream);
+}

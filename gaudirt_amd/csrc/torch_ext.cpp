@@ -454,6 +454,7 @@ at::Tensor paged_attn_validated(const at::Tensor& query, const at::Tensor& key, 
            "GaudiRT attention: KV store");
   const int32_t* words = plan.storage.data_ptr<int32_t>();
   gk_decode_params p{};
+  p.struct_size = sizeof(p);
   p.query = q.data_ptr();
   p.q_row_stride = q.stride(0);
   p.pool = pool;

@@ -3,7 +3,9 @@
  *
  * Every entry point takes plain pointers, sizes and a hipStream_t, enqueues its
  * work on that stream and returns a status code (GK_OK on success); no C++
- * exception crosses this boundary. On failure gk_last_error() returns a
+ * exception crosses this boundary. Parameter structs begin with struct_size,
+ * which the caller sets to sizeof the struct it was compiled with: a caller
+ * built against another version of this header is rejected, not misread. On failure gk_last_error() returns a
  * message for the calling thread. Arguments are validated on the host before
  * anything is enqueued, so a rejected call has written nothing.
  *
@@ -68,6 +70,7 @@ int gk_kv_store(const void* key, const void* value, int64_t key_row_stride, int6
  * (optionally capped: softcap * tanh(s / softcap)); output bf16.
  * ------------------------------------------------------------------------- */
 typedef struct gk_decode_params {
+  size_t struct_size;          /* sizeof(gk_decode_params) as the caller was built; checked */
   const void* query;           /* bf16 [rows, q_row_stride]; heads contiguous in a row */
   int64_t q_row_stride;        /* elements */
   const void* pool;            /* head-major combined KV pool of one layer */
@@ -92,6 +95,9 @@ typedef struct gk_decode_params {
   const void* new_value;
   int64_t new_kv_row_stride;
   const int32_t* slot_mapping;
+  /* Optional [rows]: query/output row of work row r (NULL = r), so decode can
+   * serve a subset of a batch's rows. row_request/row_context stay per work row. */
+  const int32_t* row_map;
 } gk_decode_params;
 
 /* Workspace bytes gk_paged_decode needs for these parameters (0 if none). */
@@ -100,6 +106,43 @@ size_t gk_paged_decode_workspace_bytes(const gk_decode_params* params);
 int32_t gk_paged_decode_partition_tokens(const gk_decode_params* params);
 int gk_paged_decode(const gk_decode_params* params, void* workspace, size_t workspace_bytes,
                     hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Chunked / prefix-shared prefill attention with bf16 MFMA. Replaces the
+ * prefill blocks of src/bridge/paged_attention.cpp:264-345 (query blocks of up
+ * to 256-512 rows over 512-key tiles, src/bridge/attention_plan.cpp:199-237).
+ *
+ * Sequence s contributes seq_rows[s] consecutive query rows starting at row
+ * seq_first_row[s], at positions seq_prefix[s] + i; row i attends keys
+ * [left, seq_prefix[s] + i] of block-table row seq_request[s] (causal; left =
+ * position - sliding_window + 1 when a window is set, else 0). Every key,
+ * including the chunk's own, must already be in the pool (store first).
+ * head_dim 64 or 128; GQA group at most 128; block_size a power of two >= 32.
+ * ------------------------------------------------------------------------- */
+typedef struct gk_prefill_params {
+  size_t struct_size;          /* sizeof(gk_prefill_params) as the caller was built; checked */
+  const void* query;           /* bf16 [rows, q_row_stride] */
+  int64_t q_row_stride;
+  const void* pool;
+  int64_t slots;
+  const int32_t* block_tables; /* [requests, bt_stride] */
+  int64_t bt_stride;
+  int32_t block_size;
+  const int32_t* seq_request;   /* [seqs] */
+  const int32_t* seq_first_row; /* [seqs] */
+  const int32_t* seq_rows;      /* [seqs] */
+  const int32_t* seq_prefix;    /* [seqs] position of the chunk's first row */
+  int32_t seqs;
+  int32_t max_rows;             /* host bound: seq_rows[s] <= max_rows */
+  int32_t q_heads, kv_heads, head_dim;
+  float scale;
+  float softcap;
+  int32_t sliding_window;
+  void* out;                    /* bf16 [rows, out_row_stride] */
+  int64_t out_row_stride;
+} gk_prefill_params;
+
+int gk_paged_prefill(const gk_prefill_params* params, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Split-K merge on its own: combines `parts` fp32 partial states per (row, head)

@@ -81,3 +81,34 @@ def kv_store(key, value, slot_mapping, pool, kv_heads, head_dim):
                                value.stride(0), ctypes.c_void_p(slot_mapping.data_ptr()), key.shape[0],
                                ctypes.c_void_p(pool.data_ptr()), pool.shape[2], kv_heads, head_dim,
                                capi.current_stream()))
+
+
+def prefill_params(query, pool, tables, seq_request, seq_first_row, seq_rows, seq_prefix, heads, kv_heads,
+                   head_dim, block_size, scale, out, max_rows, softcap=0.0, window=-1):
+    p = capi.PrefillParams()
+    p.query, p.q_row_stride = query.data_ptr(), query.stride(0)
+    p.pool, p.slots = pool.data_ptr(), pool.shape[2]
+    p.block_tables, p.bt_stride, p.block_size = tables.data_ptr(), tables.stride(0), block_size
+    p.seq_request, p.seq_first_row = seq_request.data_ptr(), seq_first_row.data_ptr()
+    p.seq_rows, p.seq_prefix = seq_rows.data_ptr(), seq_prefix.data_ptr()
+    p.seqs, p.max_rows = seq_rows.shape[0], max_rows
+    p.q_heads, p.kv_heads, p.head_dim = heads, kv_heads, head_dim
+    p.scale, p.softcap, p.sliding_window = scale, softcap, window
+    p.out, p.out_row_stride = out.data_ptr(), out.stride(0)
+    return p
+
+
+def run_prefill_case(case):
+    """Run gk_paged_prefill on a paged_cases.PrefillCase; returns output bf16 bits [rows, Hq*d]."""
+    q = bf16_device(case.query)
+    pool = bf16_device(case.pool)
+    tables = to_device(case.block_tables)
+    seqs = len(case.chunks)
+    out = torch.full((case.rows, case.heads * case.head_dim), float("nan"), dtype=torch.bfloat16, device="cuda")
+    params = prefill_params(q, pool, tables, to_device(np.arange(seqs, dtype=np.int32)), to_device(case.first_rows),
+                            to_device(case.chunks), to_device(case.prefixes), case.heads, case.kv_heads,
+                            case.head_dim, case.block_size, case.scale, out, int(case.chunks.max()),
+                            case.softcap, case.window)
+    capi.check(capi.load().gk_paged_prefill(ctypes.byref(params), capi.current_stream()))
+    torch.cuda.synchronize()
+    return bits_of(out)

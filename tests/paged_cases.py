@@ -74,3 +74,51 @@ def host_case(device_case):
     query, pool = device_case.host_arrays()
     return DecodeCase(query, pool, device_case.tables, device_case.lens, device_case.heads,
                       device_case.kv_heads, device_case.head_dim, device_case.block_size, device_case.scale)
+
+
+class PrefillCase:
+    """Host-side chunked-prefill problem: sequences with a cached prefix plus a chunk of query rows.
+
+    Rows are concatenated per sequence; every key of every chunk (prefix and
+    chunk rows) is already in the pool, as after the store. Block tables map
+    token t of request r to slot bt[r, t // block] * block + t % block.
+    """
+
+    def __init__(self, seed, heads, kv_heads, head_dim, block_size, prefixes, chunks, num_blocks=None,
+                 shared_prefix_blocks=0, softcap=0.0, window=-1):
+        rng = np.random.default_rng(seed)
+        self.heads, self.kv_heads, self.head_dim, self.block_size = heads, kv_heads, head_dim, block_size
+        self.prefixes = np.asarray(prefixes, dtype=np.int32)
+        self.chunks = np.asarray(chunks, dtype=np.int32)
+        lens = self.prefixes + self.chunks
+        seqs = len(lens)
+        need = (lens + block_size - 1) // block_size
+        own = need - shared_prefix_blocks
+        if num_blocks is None:
+            num_blocks = shared_prefix_blocks + int(own.sum())
+        ids = rng.permutation(num_blocks).astype(np.int32)
+        shared, cursor = ids[:shared_prefix_blocks], shared_prefix_blocks
+        self.block_tables = np.full((seqs, int(need.max())), -1, dtype=np.int32)
+        for s in range(seqs):
+            self.block_tables[s, :shared_prefix_blocks] = shared
+            self.block_tables[s, shared_prefix_blocks:need[s]] = ids[cursor:cursor + own[s]]
+            cursor += own[s]
+        self.pool = bf16_normal(rng, (2, kv_heads, num_blocks * block_size, head_dim))
+        self.first_rows = np.concatenate([[0], np.cumsum(self.chunks)[:-1]]).astype(np.int32)
+        self.rows = int(self.chunks.sum())
+        self.query = bf16_normal(rng, (self.rows, heads * head_dim))
+        self.scale = float(np.float32(1 / math.sqrt(head_dim)))
+        self.softcap, self.window = softcap, window
+        self.requests = np.repeat(np.arange(seqs), self.chunks).astype(np.int64)
+        self.positions = np.concatenate([p + np.arange(c) for p, c in zip(self.prefixes, self.chunks)]).astype(np.int64)
+
+    @property
+    def slots(self):
+        return self.pool.shape[2]
+
+    def oracle_problem(self, rows=None):
+        context = int((self.prefixes + self.chunks).max())
+        mapping = orc.mapping_from_block_table(self.block_tables, self.block_size, context)
+        sel = np.arange(self.rows) if rows is None else np.asarray(rows)
+        return orc.Problem(self.query[sel], self.pool, self.requests[sel], self.positions[sel], mapping,
+                           self.heads, self.kv_heads, self.head_dim, self.scale, self.softcap, self.window)

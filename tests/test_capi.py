@@ -72,3 +72,18 @@ def test_kv_store_validation(lib):
     rc = lib.gk_kv_store(None, None, 128, 128, None, 4, None, 64, 1, 100, None)
     assert rc == capi.GK_ERR_INVALID_ARGUMENT and "geometry" in lib.gk_last_error().decode()
     assert lib.gk_kv_store(None, None, 128, 128, None, 0, None, 64, 1, 128, None) == capi.GK_OK
+
+
+def test_struct_size_guard_rejects_mismatched_callers(lib):
+    # A caller compiled against another layout of gk_decode_params is rejected
+    # before any field past struct_size is read.
+    p = capi.DecodeParams()
+    p.rows, p.q_heads, p.kv_heads, p.head_dim, p.block_size, p.slots, p.scale = 1, 8, 2, 128, 128, 8192, 0.1
+    p.struct_size = ctypes.sizeof(p) - 8
+    assert lib.gk_paged_decode(ctypes.byref(p), None, 0, None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "struct_size" in lib.gk_last_error().decode()
+    assert lib.gk_paged_decode_workspace_bytes(ctypes.byref(p)) == 0
+    q = capi.PrefillParams()
+    q.struct_size = 8
+    assert lib.gk_paged_prefill(ctypes.byref(q), None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "struct_size" in lib.gk_last_error().decode()

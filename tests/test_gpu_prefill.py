@@ -1,0 +1,114 @@
+"""GPU parity of the MFMA chunked / prefix-shared prefill (gk_paged_prefill) against the CPU oracle.
+
+Cases follow the reference's prefill coverage: chunked prefill over a cached
+prefix (tests/paged_attention_same_prefix_smoke.py), the last chunked row
+against a single-row decode on the same prefix
+(tests/paged_attention_prefix_equivalence_smoke.py), GQA geometries, sliding
+window / softcap (tests/paged_attention_generalized_smoke.py) and poisoned
+unused slots (tests/multitile_paged_attention_unit_test.cpp:1722-1767).
+BASELINE config 3 (8 x 512-row chunks on a shared 2048-token prefix) is run at
+full size and checked on sampled rows plus the cross-path property.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import paged_cases as cases
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+@pytest.fixture(scope="module")
+def runner():
+    import torch
+    assert torch.cuda.is_available()
+    from tests import gk_runner
+    return gk_runner
+
+
+def check(case, actual, rows=None, fp32_softmax=False):
+    sel = np.arange(case.rows) if rows is None else np.asarray(rows)
+    p = case.oracle_problem(sel)
+    ref = orc.fp32_softmax_attention(p) if fp32_softmax else orc.direct_bf16_pv(p)
+    got = actual[sel]
+    assert np.isfinite(orc.bf16_to_f32(got)).all()
+    max_abs, mean_abs = orc.check_tolerance(got, ref, MAX_ABS, MEAN_ABS)
+    if not fp32_softmax:
+        orc.isolated_errors(orc.bf16_to_f32(got), orc.fp64_bf16(p), orc.bf16_to_f32(orc.tiled_bf16_pv(p, 512)))
+    return max_abs, mean_abs
+
+
+@pytest.mark.parametrize("geometry", [(32, 8, 128), (8, 8, 64), (14, 2, 64), (64, 8, 128), (128, 1, 64),
+                                      (4, 4, 128), (24, 3, 128)])
+def test_prefill_geometries(runner, geometry):
+    heads, kv_heads, d = geometry
+    case = cases.PrefillCase(heads + kv_heads, heads, kv_heads, d, 64, prefixes=[0, 37, 300, 64],
+                             chunks=[1, 45, 130, 77])
+    print("geometry", geometry, check(case, runner.run_prefill_case(case)), flush=True)
+
+
+@pytest.mark.parametrize("block_size", [32, 128, 256])
+def test_prefill_block_sizes(runner, block_size):
+    case = cases.PrefillCase(block_size, 32, 8, 128, block_size, prefixes=[5, 600, 0], chunks=[300, 31, 129])
+    check(case, runner.run_prefill_case(case))
+
+
+def test_prefill_shared_prefix_small(runner):
+    case = cases.PrefillCase(4, 32, 8, 128, 128, prefixes=[256] * 4, chunks=[64, 65, 1, 100],
+                             shared_prefix_blocks=2)
+    check(case, runner.run_prefill_case(case))
+
+
+@pytest.mark.parametrize("variant", ["window", "softcap"])
+def test_prefill_window_and_softcap(runner, variant):
+    case = cases.PrefillCase(9, 16, 4, 128, 32, prefixes=[100, 0, 333], chunks=[90, 200, 17],
+                             softcap=40.0 if variant == "softcap" else 0.0,
+                             window=70 if variant == "window" else -1)
+    check(case, runner.run_prefill_case(case), fp32_softmax=True)
+
+
+def test_prefill_poisoned_unused_slots(runner):
+    case = cases.PrefillCase(21, 32, 8, 128, 64, prefixes=[10, 70], chunks=[50, 33], num_blocks=16)
+    used = np.zeros(case.slots, dtype=bool)
+    for r, p in zip(case.requests, case.positions):
+        for t in range(p + 1):
+            used[case.block_tables[r, t // 64] * 64 + t % 64] = True
+    case.pool[:, :, ~used, :] = 0x7fc0
+    check(case, runner.run_prefill_case(case))
+
+
+def test_prefill_rejects_small_blocks(runner):
+    from gaudirt_amd import capi
+    import torch
+    p = capi.PrefillParams()
+    p.head_dim, p.q_heads, p.kv_heads, p.block_size, p.slots, p.scale = 128, 8, 2, 16, 1024, 0.1
+    assert capi.load().gk_paged_prefill(ctypes.byref(p), None) == capi.GK_ERR_UNSUPPORTED
+    del torch
+
+
+def test_c4_prefix_shared_chunked_prefill(runner):
+    """BASELINE config 3 at full size: 8 sequences, shared 2048-token prefix
+    (identical block ids 0..15 of the pool), 512-row causal chunks, 32 q / 8 kv
+    heads, d 128. Sampled rows against the oracle; every chunk's last row
+    against a single-row decode over the same prefix (cross-path property)."""
+    import torch
+
+    case = cases.PrefillCase(2026, 32, 8, 128, 128, prefixes=[2048] * 8, chunks=[512] * 8, shared_prefix_blocks=16)
+    actual = runner.run_prefill_case(case)
+    rng = np.random.default_rng(3)
+    sample = np.unique(np.concatenate([case.first_rows, case.first_rows + 511,
+                                       rng.integers(0, case.rows, 40)]))
+    print("c4 sampled rows", check(case, actual, sample), flush=True)
+    # decode of each chunk's last row over the same keys
+    last = case.first_rows + case.chunks - 1
+    dcase = cases.DecodeCase(case.query[last], case.pool, case.block_tables, (case.positions[last] + 1).astype(np.int32),
+                             32, 8, 128, 128)
+    decoded = runner.run_case(dcase)
+    max_abs, _ = orc.tolerance_errors(decoded, actual[last])
+    assert max_abs <= 1e-2, max_abs
+    del torch
