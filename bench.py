@@ -38,7 +38,10 @@ WORKLOADS = {
     "c3": "fused KV store + decode: batch 256, 32 q / 8 kv heads, head_dim 128, block 128, len U[128,2048]",
     "c5": "70B-shaped long decode: batch 32, 64 q / 8 kv heads, head_dim 128, block 128, "
           "ctx log-U[1024,32768], 8192-block pool, split-K",
+    "c4": "prefix-shared chunked prefill: 8 sequences x 512-row causal chunks on a shared 2048-token prefix, "
+          "32 q / 8 kv heads, head_dim 128, block 128",
 }
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def parse_args():
@@ -94,12 +97,60 @@ def cpu_baseline(dc, target_seconds):
     }
 
 
+def prefill_bench(args):
+    """one gk_paged_prefill call per step; MFMA roofline (causal-exact FLOPs)."""
+    import torch
+
+    from gaudirt_amd import capi, workloads
+
+    lib = capi.load()
+    pc = workloads.DevicePrefillCase(seed=args.seed)
+    stream = torch.cuda.current_stream()
+    p = capi.PrefillParams()
+    p.query, p.q_row_stride = pc.query.data_ptr(), pc.query.stride(0)
+    p.pool, p.slots = pc.pool.data_ptr(), pc.slots
+    p.block_tables, p.bt_stride, p.block_size = pc.d_tables.data_ptr(), pc.d_tables.stride(0), pc.block_size
+    p.seq_request, p.seq_first_row = pc.seq_request.data_ptr(), pc.seq_first_row.data_ptr()
+    p.seq_rows, p.seq_prefix = pc.seq_rows.data_ptr(), pc.seq_prefix.data_ptr()
+    p.seqs, p.max_rows = pc.seqs, pc.chunk
+    p.q_heads, p.kv_heads, p.head_dim = pc.heads, pc.kv_heads, pc.head_dim
+    p.scale, p.softcap, p.sliding_window = pc.scale, 0.0, -1
+    p.out, p.out_row_stride = pc.out.data_ptr(), pc.out.stride(0)
+    hstream = ctypes.c_void_p(stream.cuda_stream)
+    for _ in range(args.warmup):
+        capi.check(lib.gk_paged_prefill(ctypes.byref(p), hstream))
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        capi.check(lib.gk_paged_prefill(ctypes.byref(p), hstream))
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    tflops = pc.flops() / (ms * 1e-3) / 1e12
+    print(f"[bench] c4: {ms * 1e3:.1f} us/step, {tflops:.1f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of "
+          f"{MFMA_BF16_PEAK_TFLOPS:.0f}), {pc.rows / (ms * 1e-3):.4g} query rows/s", file=sys.stderr, flush=True)
+    print(json.dumps({
+        "metric": "prefix-shared chunked prefill attention TFLOP/s (causal-exact), 1 MI355X",
+        "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic", "config": {"workload": f"c4: {WORKLOADS['c4']}", "flops_per_step": pc.flops()},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None},
+        "cpu_baseline": None}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the decode path does not shard across GPUs here", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "c4":
+        import torch
+        assert torch.cuda.is_available(), "bench.py needs an MI355X"
+        torch.cuda.set_device(0)
+        return prefill_bench(args)
 
     import numpy as np
     import torch

@@ -143,12 +143,22 @@ pybind11::dict allocator_stats(int64_t device) {
 // ---------------------------------------------------------------------------
 struct PlanInfo {
   int64_t rows = 0, query_heads = 0, kv_heads = 0, head_dim = 0, slots = 0;
-  int64_t block_size = 1, bt_stride = 0, requests = 0, max_context = 0, sliding_window = -1;
+  int64_t block_size = 1, bt_stride = 0, requests = 0, sliding_window = -1;
   int device = 0;
   hipStream_t stream = nullptr;
   at::Tensor storage;  // the plan's own device buffer
-  int64_t row_request_offset = 0, row_context_offset = 0, block_table_offset = 0;
+  int64_t block_table_offset = 0;
+  // Rows attended one by one (gk_paged_decode): request, visible keys and the
+  // batch row of each.
+  int64_t decode_rows = 0, decode_max_context = 0;
+  int64_t row_request_offset = 0, row_context_offset = 0, row_map_offset = 0;
+  // Runs of consecutive positions attended as MFMA tiles (gk_paged_prefill).
+  int64_t prefill_seqs = 0, prefill_max_rows = 0;
+  int64_t seq_request_offset = 0, seq_first_row_offset = 0, seq_rows_offset = 0, seq_prefix_offset = 0;
 };
+
+// Runs of at least this many consecutive positions go to the prefill kernel.
+constexpr int64_t kPrefillMinRows = 8;
 
 void release_plan(void* ctx) { delete static_cast<PlanInfo*>(ctx); }
 
@@ -326,23 +336,46 @@ class PagedMetadata : public torch::CustomClassHolder {
     for (int64_t r = 0; r < request_count_; ++r)
       for (int64_t t = 0; t <= max_position_[r]; t += page)
         tables[r * max_pages + t / page] = mapping_h_[r * context_ + t] / static_cast<int32_t>(page);
-    std::vector<int32_t> words;
-    words.reserve(2 * rows_ + tables.size());
-    info->row_request_offset = 0;
-    words.insert(words.end(), requests_h_.begin(), requests_h_.end());
-    info->row_context_offset = rows_;
-    int64_t max_context = 0;
-    for (int64_t i = 0; i < rows_; ++i) {
-      words.push_back(positions_h_[i] + 1);
-      max_context = std::max<int64_t>(max_context, positions_h_[i] + 1);
+    // Split the rows: runs of >= kPrefillMinRows consecutive positions become
+    // prefill sequences (MFMA tiles of rows x heads) when the prefill kernel
+    // supports the geometry; every other row is a decode row.
+    const bool prefill_ok = (head_dim == 64 || head_dim == 128) && page >= 32 && query_heads / kv_heads <= 128;
+    std::vector<int32_t> dec_request, dec_context, dec_map, seq_request, seq_first, seq_rows, seq_prefix;
+    for (const auto& run : sequences_) {
+      if (prefill_ok && run.length >= kPrefillMinRows) {
+        seq_request.push_back(requests_h_[run.row]);
+        seq_first.push_back(run.row);
+        seq_rows.push_back(run.length);
+        seq_prefix.push_back(run.prefix);
+        info->prefill_max_rows = std::max<int64_t>(info->prefill_max_rows, run.length);
+        continue;
+      }
+      for (int32_t i = run.row; i < run.row + run.length; ++i) {
+        dec_request.push_back(requests_h_[i]);
+        dec_context.push_back(positions_h_[i] + 1);
+        dec_map.push_back(i);
+        info->decode_max_context = std::max<int64_t>(info->decode_max_context, positions_h_[i] + 1);
+      }
     }
-    // keep the block tables 16-byte aligned
-    while (words.size() % 4) words.push_back(0);
-    info->block_table_offset = static_cast<int64_t>(words.size());
-    words.insert(words.end(), tables.begin(), tables.end());
+    std::vector<int32_t> words;
+    const auto append = [&](const std::vector<int32_t>& v) {
+      while (words.size() % 4) words.push_back(0);  // 16-byte aligned sections
+      const auto offset = static_cast<int64_t>(words.size());
+      words.insert(words.end(), v.begin(), v.end());
+      return offset;
+    };
+    info->decode_rows = static_cast<int64_t>(dec_map.size());
+    info->row_request_offset = append(dec_request);
+    info->row_context_offset = append(dec_context);
+    info->row_map_offset = append(dec_map);
+    info->prefill_seqs = static_cast<int64_t>(seq_rows.size());
+    info->seq_request_offset = append(seq_request);
+    info->seq_first_row_offset = append(seq_first);
+    info->seq_rows_offset = append(seq_rows);
+    info->seq_prefix_offset = append(seq_prefix);
+    info->block_table_offset = append(tables);
     info->block_size = page;
     info->bt_stride = max_pages;
-    info->max_context = max_context;
     auto host = at::from_blob(words.data(), {static_cast<int64_t>(words.size())}, at::TensorOptions().dtype(at::kInt));
     info->storage = host.to(device_int32().device(), false, true);
     auto plan = make_plan_tensor(std::move(info));
@@ -453,31 +486,61 @@ at::Tensor paged_attn_validated(const at::Tensor& query, const at::Tensor& key, 
                        static_cast<int32_t>(head_dim), stream),
            "GaudiRT attention: KV store");
   const int32_t* words = plan.storage.data_ptr<int32_t>();
-  gk_decode_params p{};
-  p.struct_size = sizeof(p);
-  p.query = q.data_ptr();
-  p.q_row_stride = q.stride(0);
-  p.pool = pool;
-  p.slots = plan.slots;
-  p.block_tables = words + plan.block_table_offset;
-  p.bt_stride = plan.bt_stride;
-  p.block_size = static_cast<int32_t>(plan.block_size);
-  p.row_request = words + plan.row_request_offset;
-  p.row_context = words + plan.row_context_offset;
-  p.rows = static_cast<int32_t>(plan.rows);
-  p.q_heads = static_cast<int32_t>(plan.query_heads);
-  p.kv_heads = static_cast<int32_t>(plan.kv_heads);
-  p.head_dim = static_cast<int32_t>(head_dim);
-  p.scale = scale_f;
-  p.softcap = softcap_f;
-  p.sliding_window = sliding_window > 0 ? static_cast<int32_t>(sliding_window) : -1;
-  p.max_context = static_cast<int32_t>(plan.max_context);
-  p.out = output.data_ptr();
-  p.out_row_stride = output.stride(0);
-  const size_t need = gk_paged_decode_workspace_bytes(&p);
-  at::Tensor workspace;
-  if (need) workspace = at::empty({static_cast<int64_t>(need)}, query.options().dtype(at::kByte));
-  check_gk(gk_paged_decode(&p, need ? workspace.data_ptr() : nullptr, need, stream), "GaudiRT attention");
+  const int32_t sw = sliding_window > 0 ? static_cast<int32_t>(sliding_window) : -1;
+  if (plan.prefill_seqs) {
+    gk_prefill_params f{};
+    f.struct_size = sizeof(f);
+    f.query = q.data_ptr();
+    f.q_row_stride = q.stride(0);
+    f.pool = pool;
+    f.slots = plan.slots;
+    f.block_tables = words + plan.block_table_offset;
+    f.bt_stride = plan.bt_stride;
+    f.block_size = static_cast<int32_t>(plan.block_size);
+    f.seq_request = words + plan.seq_request_offset;
+    f.seq_first_row = words + plan.seq_first_row_offset;
+    f.seq_rows = words + plan.seq_rows_offset;
+    f.seq_prefix = words + plan.seq_prefix_offset;
+    f.seqs = static_cast<int32_t>(plan.prefill_seqs);
+    f.max_rows = static_cast<int32_t>(plan.prefill_max_rows);
+    f.q_heads = static_cast<int32_t>(plan.query_heads);
+    f.kv_heads = static_cast<int32_t>(plan.kv_heads);
+    f.head_dim = static_cast<int32_t>(head_dim);
+    f.scale = scale_f;
+    f.softcap = softcap_f;
+    f.sliding_window = sw;
+    f.out = output.data_ptr();
+    f.out_row_stride = output.stride(0);
+    check_gk(gk_paged_prefill(&f, stream), "GaudiRT attention (prefill)");
+  }
+  if (plan.decode_rows) {
+    gk_decode_params p{};
+    p.struct_size = sizeof(p);
+    p.query = q.data_ptr();
+    p.q_row_stride = q.stride(0);
+    p.pool = pool;
+    p.slots = plan.slots;
+    p.block_tables = words + plan.block_table_offset;
+    p.bt_stride = plan.bt_stride;
+    p.block_size = static_cast<int32_t>(plan.block_size);
+    p.row_request = words + plan.row_request_offset;
+    p.row_context = words + plan.row_context_offset;
+    p.row_map = words + plan.row_map_offset;
+    p.rows = static_cast<int32_t>(plan.decode_rows);
+    p.q_heads = static_cast<int32_t>(plan.query_heads);
+    p.kv_heads = static_cast<int32_t>(plan.kv_heads);
+    p.head_dim = static_cast<int32_t>(head_dim);
+    p.scale = scale_f;
+    p.softcap = softcap_f;
+    p.sliding_window = sw;
+    p.max_context = static_cast<int32_t>(plan.decode_max_context);
+    p.out = output.data_ptr();
+    p.out_row_stride = output.stride(0);
+    const size_t need = gk_paged_decode_workspace_bytes(&p);
+    at::Tensor workspace;
+    if (need) workspace = at::empty({static_cast<int64_t>(need)}, query.options().dtype(at::kByte));
+    check_gk(gk_paged_decode(&p, need ? workspace.data_ptr() : nullptr, need, stream), "GaudiRT attention");
+  }
   return output;
 }
 

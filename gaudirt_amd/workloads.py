@@ -108,3 +108,52 @@ class DeviceDecodeCase:
         pool = self.pool.view(torch.int16).cpu().numpy().view(np.uint16)
         query = self.query.view(torch.int16).cpu().numpy().view(np.uint16)
         return query, pool
+
+
+class DevicePrefillCase:
+    """BASELINE config 3 on the GPU: prefix-shared chunked prefill.
+
+    `seqs` sequences share a `prefix`-token prefix through identical block ids
+    (the first prefix/block blocks of every table), each adds `chunk` causal
+    query rows with blocks of its own. The pool already holds every key (as
+    after the store), filled with bf16 N(0, 1).
+    """
+
+    def __init__(self, seqs=8, prefix=2048, chunk=512, heads=32, kv_heads=8, head_dim=128, block=128, seed=1234,
+                 device="cuda"):
+        import torch
+
+        rng = np.random.default_rng(seed)
+        self.seqs, self.prefix, self.chunk = seqs, prefix, chunk
+        self.heads, self.kv_heads, self.head_dim, self.block_size = heads, kv_heads, head_dim, block
+        shared = prefix // block
+        own = (prefix + chunk + block - 1) // block - shared
+        num_blocks = shared + seqs * own
+        ids = rng.permutation(num_blocks).astype(np.int32)
+        tables = np.empty((seqs, shared + own), dtype=np.int32)
+        tables[:, :shared] = ids[:shared]
+        for s in range(seqs):
+            tables[s, shared:] = ids[shared + s * own:shared + (s + 1) * own]
+        self.tables = tables
+        self.slots = num_blocks * block
+        self.rows = seqs * chunk
+        self.scale = float(np.float32(1 / math.sqrt(head_dim)))
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        self.pool = torch.empty((2, kv_heads, self.slots, head_dim), dtype=torch.bfloat16, device=device)
+        for kind in range(2):
+            for h in range(kv_heads):
+                self.pool[kind, h].normal_(generator=gen)
+        self.query = torch.randn((self.rows, heads * head_dim), generator=gen, device=device).to(torch.bfloat16)
+        self.out = torch.empty_like(self.query)
+        i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(device)
+        self.d_tables = i32(tables)
+        self.seq_request = i32(np.arange(seqs))
+        self.seq_first_row = i32(np.arange(seqs) * chunk)
+        self.seq_rows = i32(np.full(seqs, chunk))
+        self.seq_prefix = i32(np.full(seqs, prefix))
+
+    def flops(self):
+        """Causal-exact FLOPs: every visible (query, key) pair costs 4 d (Q.K and P.V)."""
+        pairs = sum(self.prefix + i + 1 for i in range(self.chunk))
+        return 4 * self.head_dim * self.heads * self.seqs * pairs

@@ -210,3 +210,53 @@ def test_kv_pool_allocation_and_reuse(torch_ext):
     assert gaudirt_amd.kv_allocator_stats(0)["allocated_bytes"] < before
     with pytest.raises(RuntimeError, match="unsupported head-major KV pool geometry"):
         gaudirt_amd.allocate_paged_kv(1, 100, 2, 96)
+
+
+@pytest.mark.parametrize("heads,kv_heads,dim,block", [(32, 8, 128, 64), (8, 2, 64, 128), (16, 16, 128, 32)])
+def test_mixed_prefill_and_decode_batch(torch_ext, heads, kv_heads, dim, block):
+    """A batch mixing chunked-prefill runs (>= 8 consecutive positions: MFMA
+    prefill kernel) and single decode rows (decode kernel via row_map), with a
+    page-aligned request map, as a serving step of the reference would send
+    (tests/paged_layer_store_smoke.py: mixed fused and tiled blocks with one
+    KV update)."""
+    import gaudirt_amd
+
+    torch = torch_ext
+    rng = np.random.default_rng(heads * 7 + block)
+    requests_n = 6
+    prefix = [0, 130, 7, 500, 64, 300]
+    chunk = [40, 9, 1, 3, 200, 1]     # runs of 40, 9 and 200 rows go to prefill
+    lens = [p + c for p, c in zip(prefix, chunk)]
+    blocks_per = [(n + block - 1) // block for n in lens]
+    ids = rng.permutation(sum(blocks_per) + 5)
+    context = max(lens)
+    mapping = np.full((requests_n, context), -1, dtype=np.int32)
+    cursor = 0
+    for r in range(requests_n):
+        for t in range(lens[r]):
+            mapping[r, t] = ids[cursor + t // block] * block + t % block
+        cursor += blocks_per[r]
+    slots = (sum(blocks_per) + 5) * block
+    req = np.concatenate([np.full(c, r) for r, c in enumerate(chunk)]).astype(np.int64)
+    pos = np.concatenate([p + np.arange(c) for p, c in zip(prefix, chunk)]).astype(np.int64)
+    loc = mapping[req, pos].astype(np.int64)
+    rows = len(req)
+    meta = torch.classes.gaudirt.PagedMetadata(torch.from_numpy(loc), torch.from_numpy(req), torch.from_numpy(pos),
+                                               torch.from_numpy(mapping), slots)
+    gen = torch.Generator().manual_seed(5)
+    q_cpu = randn_bf16(torch, gen, rows, heads * dim)
+    k_cpu = randn_bf16(torch, gen, rows, kv_heads * dim)
+    v_cpu = randn_bf16(torch, gen, rows, kv_heads * dim)
+    pool = gaudirt_amd.allocate_paged_kv(1, slots, kv_heads, dim)
+    base = randn_bf16(torch, gen, 2, kv_heads, slots, dim)
+    pool[0].copy_(base)
+    key_pool, value_pool = gaudirt_amd.kv_pool_views(pool, 0)
+    scale = float(np.float32(1 / math.sqrt(dim)))
+    out = torch.ops.gaudirt.paged_attn.default(q_cpu.cuda(), k_cpu.cuda(), v_cpu.cuda(), key_pool, value_pool,
+                                               meta, dim, scale)
+    torch.cuda.synchronize()
+    expected = bits(base)
+    orc.kv_store(bits(k_cpu), bits(v_cpu), loc, rows, expected, slots, kv_heads, dim)
+    assert np.array_equal(bits(pool[0]), expected)
+    problem = orc.Problem(bits(q_cpu), expected, req, pos, mapping, heads, kv_heads, dim, scale)
+    print("mixed batch", check(bits(out), problem), flush=True)
