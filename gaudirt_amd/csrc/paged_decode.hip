@@ -31,7 +31,7 @@
 // log-sum-exp rule. A row with a single partition is finalised in place.
 //
 // Numerics versus the reference (src/bridge/paged_attention.cpp:99-122 and the
-// tile chain of src/bridge/paged_attention_tiles.cpp:189-219): scores are fp32
+// tile chain of src/bridge/paged_attention_tiles.cpp:157-188): scores are fp32
 // q.k times scale; probabilities are rounded to bf16 before P.V as in the
 // reference, but relative to a running rather than the final max, and
 // normalised once at the end; sums use the unrounded fp32 probabilities.

@@ -20,7 +20,7 @@
 // Online softmax runs in log2 units with a lazily re-based running maximum.
 //
 // Numerics versus the reference (the tile chain of
-// src/bridge/paged_attention_tiles.cpp:87-225): fp32 scores times scale,
+// src/bridge/paged_attention_tiles.cpp:57-195): fp32 scores times scale,
 // probabilities rounded to bf16 before P.V (relative to the running maximum),
 // fp32 accumulation, one normalisation at the end, bf16 output.
 #include "gk_mfma.hpp"

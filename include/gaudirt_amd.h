@@ -40,14 +40,15 @@ enum {
   GK_ERR_WORKSPACE = 5,
 };
 
-/* Message of the last failed call on this thread ("" if none). */
+/* Message of the last failed call on this thread ("" if none). No counterpart
+ * in the reference, which reports errors through TORCH_CHECK exceptions. */
 const char* gk_last_error(void);
-/* Library version string. */
+/* Library version string. No counterpart in the reference. */
 const char* gk_version(void);
 
 /* ---------------------------------------------------------------------------
  * KV store. Replaces the gk_kv_store_head_major_bf16_v1 launch of
- * src/bridge/paged_attention_tiles.cpp:266-290 (recipe :67-85, fused variant
+ * src/bridge/paged_attention_tiles.cpp:236-260 (recipe :37-55, fused variant
  * src/bridge/paged_attention.cpp:66-76): for r < rows and every kv head, the
  * row's head slice of key/value is written to slot slot_mapping[r] of the pool.
  * A negative slot skips the row; every other pool byte is untouched.
@@ -61,7 +62,7 @@ int gk_kv_store(const void* key, const void* value, int64_t key_row_stride, int6
  * Paged decode attention over block tables with split-K partitions and a
  * second-pass log-sum-exp merge. Replaces the fused single-tile recipe and the
  * multi-tile chunk chain of src/bridge/paged_attention.cpp:39-127,264-345 and
- * src/bridge/paged_attention_tiles.cpp:87-225,292-389 (tile softmax,
+ * src/bridge/paged_attention_tiles.cpp:57-195,262-359 (tile softmax,
  * gk_attn_online_merge_f32_v1, gk_attn_online_finalize_bf16_v1).
  *
  * Each query row r attends keys [left, row_context[r]) of request
@@ -150,7 +151,7 @@ int gk_paged_prefill(const gk_prefill_params* params, hipStream_t stream);
  * unnormalised sums sum_t 2^(s_t - m) v_t; partial_ml [rows, heads, max_parts, 2]
  * holds (m, l) with m in log2 units and l = sum_t 2^(s_t - m); part_count[r] is
  * the number of valid parts of row r. Replaces gk_attn_online_merge_f32_v1 and
- * gk_attn_online_finalize_bf16_v1 (src/bridge/paged_attention_tiles.cpp:164-190).
+ * gk_attn_online_finalize_bf16_v1 (src/bridge/paged_attention_tiles.cpp:173-188).
  * ------------------------------------------------------------------------- */
 int gk_split_k_merge(const float* partial_out, const float* partial_ml, const int32_t* part_count,
                      int32_t rows, int32_t heads, int32_t max_parts, int32_t head_dim, void* out,
