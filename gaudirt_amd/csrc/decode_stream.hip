@@ -1,0 +1,684 @@
+// Balanced paged decode for gfx950 ("stream" schedule).
+//
+// The grid holds exactly as many one-wave workgroups as the GPU keeps resident.
+// All key tiles of the batch form one sequence: work units (row, kv head, head
+// group) in row-major order, each unit's tiles in key order. Workgroup w takes
+// the contiguous range [w * per, (w + 1) * per) of that sequence, so every
+// workgroup streams the same number of K/V bytes however skewed the context
+// lengths are, and its two-stage LDS pipeline runs without a break from its
+// first tile to its last: crossing into the next unit only swaps the query
+// (prefetched into LDS with that unit's first tile) and the softmax state.
+//
+// A unit whose tiles all fall in one workgroup is finalised there (bf16
+// output). A unit that spans workgroups w_first .. w_last leaves one partial
+// (unnormalised fp32 output, max and sum in log2 units) per workgroup, and the
+// merge kernel combines them with the log-sum-exp rule. Each workgroup has at
+// most two partial units (the one it starts in and the one it ends in), so the
+// partials live in 2 * wgs fixed slots: slot 2w for the segment that begins at
+// the workgroup's first tile, 2w + 1 for one that begins later.
+//
+// Tiles are TS-key ranges at absolute key positions (tile k = keys [k TS,
+// (k + 1) TS)), so with block_size >= TS every tile lies in one pool block and
+// needs one block-table entry, fetched with a scalar load one tile ahead. Keys
+// outside a row's visible range [left, ctx) are masked. Inside a unit the
+// tiles are visited rotated by kv_head * count / kv_heads: the kv heads of a
+// row then stream different blocks at any moment, instead of the same block
+// offset in regions a power-of-two apart, which concentrates the reads on a
+// subset of the HBM channels.
+//
+// The per-tile arithmetic is the partitioned MFMA kernel's (paged_decode.hip):
+// S^T = K . Q^T with v_mfma_f32_16x16x32_bf16, lazy online softmax, P rounded
+// to bf16, P . V from a transposed LDS read, both tiles loaded HBM -> LDS with
+// 16-byte buffer loads (global_load_lds_dwordx4).
+#include "decode_common.hpp"
+
+#include <algorithm>
+#include <mutex>
+
+namespace gk {
+namespace {
+
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+// One 16-byte direct load per lane, HBM -> LDS: lane l's bytes land at LDS
+// address lds + 16 l. Written as an asm statement so that the compiler's
+// wait-count model never sees the LDS side: the kernel orders every read of
+// a stage after that stage's loads with explicit vmcnt waits, and the
+// compiler's own tracking of direct loads (which cannot tell the two stages
+// apart here) would otherwise wait for the other stage's loads as well. M0
+// holds the LDS base; nothing else in this kernel uses M0 (the s_nop covers
+// the M0-write -> direct-load hazard).
+__device__ __forceinline__ void lds_dma16(uint32_t lds, __amdgpu_buffer_rsrc_t rsrc, uint32_t voffset) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds),
+      "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_char_t*)p;
+}
+
+struct StreamArgs {
+  DecodeArgs d;
+  int32_t units_per_row;  // kv_heads * head_groups
+  int32_t wgs;            // workgroups of the grid
+  float* unit_span;       // per unit: {first partial slot, last workgroup} as int32 bits
+};
+
+// A row's tiles: visible keys [left, ctx) occupy tiles first .. first + count - 1.
+// An empty row still owns one (fully masked) tile, so every unit is finalised.
+struct RowTiles {
+  int first, count, left, ctx;
+};
+
+template <int TS>
+__device__ __forceinline__ RowTiles row_tiles(int ctx, int window) {
+  RowTiles r;
+  r.ctx = ctx > 0 ? ctx : 0;
+  r.left = visible_left(r.ctx, window);
+  r.first = r.left / TS;
+  r.count = r.ctx > 0 ? (r.ctx + TS - 1) / TS - r.first : 1;
+  return r;
+}
+
+// Wave-uniform load through the scalar cache (s_load). The data is only read
+// by this kernel; the constant address space tells the compiler so, which it
+// cannot prove itself once LDS direct loads (memory writes) are in the loop.
+__device__ __forceinline__ int32_t scalar_load(const int32_t* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
+__device__ __forceinline__ int bperm(int lane_src, int x) { return __builtin_amdgcn_ds_bpermute(lane_src << 2, x); }
+
+__device__ __forceinline__ int wave_sum(int x, int lane) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x += bperm(lane ^ m, x);
+  return __builtin_amdgcn_readfirstlane(x);
+}
+
+__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = bperm(lane - d, x);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+// Position in the tile sequence, with the row data it needs (wave-uniform).
+struct Cursor {
+  int row, h, j;            // unit (row, h = kv head * head_groups + head group), tile j of the unit
+  int kvh, rot;             // the unit's kv head; rotation of its tile order
+  RowTiles rt;
+  int req, qrow;            // block-table row, query/output row
+  int64_t g;                // index in the tile sequence
+  int next_ctx, next_req, next_qrow;  // row + 1, fetched ahead
+};
+
+// What consuming one tile needs (wave-uniform).
+struct TileDesc {
+  int tb;                   // first key of the tile
+  int left, ctx;            // visible keys of the row
+  int row, h, kvh, j, count, qrow;
+  int64_t g;
+  uint32_t row0;            // byte offset of key tb in its kv head's K (and V) region
+  int q_start, q_end;       // first / last tile of the unit in this workgroup
+};
+
+template <int D, bool SOFTCAP>
+__global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
+  using S = MfmaShape<D>;
+  constexpr int TS = S::TS;
+  constexpr int QBYTES = 16 * D * 2;  // one unit's query heads (up to 16)
+  // Two K/V stages, each tile its own LDS object so that the compiler tells
+  // reads of one from the direct loads in flight into another, and the two
+  // query buffers (one object: a query read waits for the newest query load,
+  // which is never younger than the tile it comes with).
+  __shared__ __attribute__((aligned(16))) char kt0[S::TILE];
+  __shared__ __attribute__((aligned(16))) char vt0[S::TILE];
+  __shared__ __attribute__((aligned(16))) char kt1[S::TILE];
+  __shared__ __attribute__((aligned(16))) char vt1[S::TILE];
+  __shared__ __attribute__((aligned(16))) char qs[2][QBYTES];
+
+  const DecodeArgs& a = sa.d;
+  const int lane = threadIdx.x;
+  const int q = lane >> 4, c16 = lane & 15;
+  const int U = sa.units_per_row;
+  const int w = blockIdx.x;
+
+  // ---- Schedule ---------------------------------------------------------
+  // Row window: lane l holds row wb + l's context, block-table row and output row.
+  int wb = 0, wctx = 0, wreq = 0, wmap = 0;
+  auto load_window = [&](int base) {
+    wb = base;
+    const int r = base + lane;
+    wctx = 0;
+    wreq = r;
+    wmap = r;
+    if (r < a.rows) {
+      wctx = a.row_context[r];
+      if (a.row_request) wreq = a.row_request[r];
+      if (a.row_map) wmap = a.row_map[r];
+    }
+  };
+  load_window(0);
+  int64_t total = wave_sum(lane < a.rows ? row_tiles<TS>(wctx, a.window).count : 0, lane);
+  for (int base = 64; base < a.rows; base += 64) {
+    const int r = base + lane;
+    total += wave_sum(r < a.rows ? row_tiles<TS>(a.row_context[r], a.window).count : 0, lane);
+  }
+  total *= U;
+  const int64_t per = (total + sa.wgs - 1) / sa.wgs;
+  const int64_t g_begin = (int64_t)w * per;
+  const int64_t g_end = min(g_begin + per, total);
+  if (g_begin >= g_end) return;
+
+  // The row holding tile g_begin, and the sequence index of its first tile.
+  int row = 0;
+  int64_t row_base = 0;
+  int64_t pre = 0;
+  bool found = false;
+  for (int base = 0; base < a.rows; base += 64) {
+    if (base != wb) load_window(base);
+    const int r = base + lane;
+    const int n = r < a.rows ? row_tiles<TS>(wctx, a.window).count : 0;
+    const int incl = wave_inclusive_scan(n, lane);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(r < a.rows && (pre + incl) * U > g_begin);
+    if (hit) {
+      const int f = __builtin_ctzll(hit);
+      row = base + f;
+      row_base = (pre + __builtin_amdgcn_readlane(incl - n, f)) * U;
+      found = true;
+      break;
+    }
+    pre += __builtin_amdgcn_readlane(incl, 63);
+  }
+  if (!found) return;  // unreachable: g_begin < total
+
+  // A new unit's kv head and the rotation of its tile order.
+  auto enter_unit = [&](Cursor& c) {
+    c.kvh = c.h / a.head_groups;
+    c.rot = (int)((int64_t)c.kvh * c.rt.count / a.kv_heads);
+  };
+  Cursor cur;
+  {
+    const int l = row - wb;
+    cur.row = row;
+    cur.rt = row_tiles<TS>(__builtin_amdgcn_readlane(wctx, l), a.window);
+    cur.req = __builtin_amdgcn_readlane(wreq, l);
+    cur.qrow = __builtin_amdgcn_readlane(wmap, l);
+    const int64_t off = g_begin - row_base;
+    cur.h = (int)(off / cur.rt.count);
+    cur.j = (int)(off - (int64_t)cur.h * cur.rt.count);
+    cur.g = g_begin;
+    enter_unit(cur);
+    cur.next_ctx = cur.next_req = cur.next_qrow = 0;
+    if (row + 1 < a.rows) {
+      cur.next_ctx = scalar_load(a.row_context, row + 1);
+      cur.next_req = a.row_request ? scalar_load(a.row_request, row + 1) : row + 1;
+      cur.next_qrow = a.row_map ? scalar_load(a.row_map, row + 1) : row + 1;
+    }
+  }
+  auto advance = [&](Cursor& c) {
+    ++c.g;
+    if (++c.j < c.rt.count) return;
+    c.j = 0;
+    if (++c.h < U) {
+      enter_unit(c);
+      return;
+    }
+    c.h = 0;
+    ++c.row;
+    c.rt = row_tiles<TS>(c.next_ctx, a.window);
+    c.req = c.next_req;
+    c.qrow = c.next_qrow;
+    if (c.row + 1 < a.rows) {
+      c.next_ctx = scalar_load(a.row_context, c.row + 1);
+      c.next_req = a.row_request ? scalar_load(a.row_request, c.row + 1) : c.row + 1;
+      c.next_qrow = a.row_map ? scalar_load(a.row_map, c.row + 1) : c.row + 1;
+    }
+    enter_unit(c);
+  };
+  const int shift = a.block_shift;
+  const int block_mask = (1 << shift) - 1;
+  // First key of the cursor's tile (rotated order inside the unit).
+  auto tile_key = [&](const Cursor& c) {
+    int p = c.j + c.rot;
+    if (p >= c.rt.count) p -= c.rt.count;
+    return (c.rt.first + p) * TS;
+  };
+  // Block-table entry of the cursor's tile (a scalar load, issued ahead of use).
+  auto table_entry = [&](const Cursor& c) {
+    // An empty row's masked tile reads no table entry.
+    return c.rt.ctx > 0 ? scalar_load(a.block_tables, (int64_t)c.req * a.bt_stride + (tile_key(c) >> shift)) : 0;
+  };
+  auto describe = [&](const Cursor& c, int entry) {
+    TileDesc t;
+    t.tb = tile_key(c);
+    t.left = c.rt.left;
+    t.ctx = c.rt.ctx;
+    t.row = c.row;
+    t.h = c.h;
+    t.kvh = c.kvh;
+    t.j = c.j;
+    t.count = c.rt.count;
+    t.qrow = c.qrow;
+    t.g = c.g;
+    t.row0 = (((uint32_t)entry << shift) | (uint32_t)(t.tb & block_mask)) * (uint32_t)(2 * D);
+    t.q_start = c.j == 0 || c.g == g_begin;
+    t.q_end = c.j == c.rt.count - 1 || c.g == g_end - 1;
+    return t;
+  };
+
+  // ---- Loads -------------------------------------------------------------
+  const uint32_t region = (uint32_t)(a.slots * D * 2);
+  // K and V tiles -> LDS: load i, lane l fills piece s = 64 i + l, i.e. key
+  // s / CPR, stored chunk s % CPR, which holds the key's chunk (s % CPR) ^ swz.
+  auto issue_tile = [&](const TileDesc& t, char* kt, char* vt) {
+    const uint16_t* kbase = a.pool + (int64_t)t.kvh * a.slots * D;
+    const uint16_t* vbase = kbase + (int64_t)a.kv_heads * a.slots * D;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, region, kBufferDword3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, region, kBufferDword3);
+    const uint32_t kl = lds_addr(kt), vl = lds_addr(vt);
+#pragma unroll
+    for (int i = 0; i < S::LOADS; ++i) {
+      const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
+      lds_dma16(kl + i * 1024, krs, t.row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4));
+    }
+#pragma unroll
+    for (int i = 0; i < S::LOADS; ++i) {
+      const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
+      lds_dma16(vl + i * 1024, vrs, t.row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4));
+    }
+  };
+  // The unit's query heads -> LDS ([head][D], row-major). The resource covers
+  // the valid heads only, so the rest of the buffer reads as zero.
+  auto issue_query = [&](const TileDesc& t, char* qsb) {
+    const int kvh = t.kvh, hg = t.h - kvh * a.head_groups;
+    const int hv = min(16, a.group - hg * 16);
+    const uint16_t* qp = a.query + (int64_t)t.qrow * a.q_stride + (int64_t)(kvh * a.group + hg * 16) * D;
+    const uint32_t bytes = (uint32_t)(hv * D * 2);
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc((void*)qp, (short)0, bytes, kBufferDword3);
+    const uint32_t ql = lds_addr(qsb);
+#pragma unroll
+    for (int i = 0; i < QBYTES / 1024; ++i)
+      if (i * 1024 < (int)bytes) lds_dma16(ql + i * 1024, qrs, i * 1024 + lane * 16);
+  };
+
+  // ---- Attention state -----------------------------------------------------
+  bf16x8_t qb[S::NC];
+  f32x4_t o[S::NO];
+  float m_run = -INFINITY, l_run = 0.f;
+
+  auto finalize = [&](const TileDesc& t) {
+    l_run += shfl_xor(l_run, 16);
+    l_run += shfl_xor(l_run, 32);
+    float lrow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      lrow[r] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l_run)));
+    const int kvh = t.kvh, hg = t.h - kvh * a.head_groups;
+    const int hv = min(16, a.group - hg * 16);
+    const int head0 = kvh * a.group + hg * 16;
+    const int64_t g0 = t.g - t.j;  // the unit's first tile
+    if (g0 >= g_begin && g0 + t.count <= g_end) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * q + r;
+        if (h >= hv) continue;
+        const float inv = lrow[r] > 0.f ? 1.f / lrow[r] : 0.f;
+        uint16_t* dst = a.out + (int64_t)t.qrow * a.out_stride + (int64_t)(head0 + h) * D + c16;
+#pragma unroll
+        for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(o[c][r] * inv);
+      }
+    } else {
+      const int slot = 2 * w + (g0 <= g_begin ? 0 : 1);
+      const int64_t pi = (int64_t)slot * a.heads_per_group;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * q + r;
+        if (h >= hv) continue;
+        float* dst = a.part_o + (pi + h) * D + c16;
+#pragma unroll
+        for (int c = 0; c < S::NO; ++c) dst[16 * c] = o[c][r];
+      }
+      if (q == 0 && c16 < hv) {
+        a.part_ml[(pi + c16) * 2] = m_run;
+        a.part_ml[(pi + c16) * 2 + 1] = l_run;
+      }
+    }
+    if (t.j == t.count - 1 && lane == 0) {
+      // This workgroup holds the unit's last tile: record where its partials are.
+      const int64_t wf = g0 / per;
+      const int first_slot = (int)(2 * wf + (g0 == wf * per ? 0 : 1));
+      float* span = sa.unit_span + ((int64_t)t.row * U + t.h) * 2;
+      span[0] = __int_as_float(first_slot);
+      span[1] = __int_as_float(w);
+    }
+  };
+
+  // Attend one tile from one stage (its loads, and its unit's query, have landed).
+  auto read_query = [&](const TileDesc& t, const char* qsb) {
+    const int hg = t.h - t.kvh * a.head_groups;
+    const int hv = min(16, a.group - hg * 16);
+#pragma unroll
+    for (int c = 0; c < S::NC; ++c) {
+      bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(qsb + c16 * (2 * D) + (4 * c + q) * 16);
+      qb[c] = c16 < hv ? v : bf16x8_t{};
+    }
+  };
+  auto consume = [&](const TileDesc& t, const char* kt, char* vt, int qpar_t) {
+    if (t.q_start) {
+      read_query(t, qs[qpar_t]);
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      m_run = -INFINITY;
+      l_run = 0.f;
+    }
+
+    // K tile -> registers as the A operand of S^T: lane (q, c16), group h holds
+    // key 16h + c16, logical chunk 4c + q.
+    bf16x8_t kr[S::TG][S::NC];
+#pragma unroll
+    for (int h = 0; h < S::TG; ++h) {
+      const int tt = 16 * h + c16;
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c)
+        kr[h][c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt)) << 4));
+    }
+    f32x4_t sc[S::TG];
+#pragma unroll
+    for (int h = 0; h < S::TG; ++h) {
+      sc[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c) sc[h] = mfma32(kr[h][c], qb[c], sc[h]);
+    }
+
+    float mx = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < S::TG; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float s;
+        if constexpr (SOFTCAP) s = a.softcap_log2 * soft_tanh(sc[h][r] * a.score_scale);
+        else s = sc[h][r] * a.score_scale;
+        const int key = t.tb + 16 * h + 4 * q + r;
+        s = (key >= t.left && key < t.ctx) ? s : -INFINITY;
+        sc[h][r] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kDecodeLazyRescale)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float f = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(alpha)));
+#pragma unroll
+        for (int c = 0; c < S::NO; ++c) o[c][r] *= f;
+      }
+    }
+    const float base = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+    for (int h = 0; h < S::TG; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = fast_exp2(sc[h][r] - base);
+        sc[h][r] = p;
+        l_run += p;
+      }
+
+    // Masked keys of a tile hold arbitrary pool data: zero their V rows so that
+    // a zero probability cannot meet a non-finite value.
+    if (t.tb < t.left || t.tb + TS > t.ctx) {
+#pragma unroll
+      for (int i = 0; i < S::LOADS; ++i) {
+        const int s = i * 64 + lane;
+        const int key = t.tb + s / S::CPR;
+        if (key < t.left || key >= t.ctx) *reinterpret_cast<uint4*>(vt + s * 16) = make_uint4(0, 0, 0, 0);
+      }
+    }
+
+    if constexpr (TS == 32) {
+      bf16x8_t pa;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pa[r] = (__bf16)sc[0][r];
+        pa[4 + r] = (__bf16)sc[1][r];
+      }
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) {
+        const int lc = 2 * c + ((c16 & 3) >> 1);
+        const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
+        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
+        const char* p1 = vt + t1 * (2 * D) + ((lc ^ swz(t1)) << 4) + ((c16 & 1) << 3);
+        const bf16x4_t v0 = lds_read_tr4(p0);
+        const bf16x4_t v1 = lds_read_tr4(p1);
+        const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[c] = mfma32(pa, vb, o[c]);
+      }
+    } else {
+      bf16x4_t pa;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pa[r] = (__bf16)sc[0][r];
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) {
+        const int lc = 2 * c + ((c16 & 3) >> 1);
+        const int t0 = 4 * q + (c16 >> 2);
+        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
+        o[c] = mfma16(pa, lds_read_tr4(p0), o[c]);
+      }
+    }
+    // The stage is refilled next: every LDS read of it must have returned.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (t.q_end) finalize(t);
+  };
+
+  // ---- Pipeline ------------------------------------------------------------
+  // Stage 0 / stage 1 alternate; the query buffer alternates per unit.
+  int64_t to_issue = g_end - g_begin;  // tiles not yet issued
+  int qpar = 0;
+  TileDesc d0 = describe(cur, table_entry(cur)), d1;
+  int qp0 = 0, qp1 = 0;                // query buffer of the tile in stage 0 / 1
+  if (d0.q_start) issue_query(d0, qs[0]);
+  issue_tile(d0, kt0, vt0);
+  --to_issue;
+  int next_entry = 0;
+  if (to_issue > 0) {
+    advance(cur);
+    next_entry = table_entry(cur);
+  }
+  while (true) {
+    bool more = to_issue > 0;
+    if (more) {
+      d1 = describe(cur, next_entry);
+      if (d1.q_start) {
+        qpar ^= 1;
+        issue_query(d1, qs[qpar]);
+      }
+      qp1 = qpar;
+      issue_tile(d1, kt1, vt1);
+      if (--to_issue > 0) {
+        advance(cur);
+        next_entry = table_entry(cur);
+      }
+      wait_vmem<2 * S::LOADS>();
+    } else {
+      wait_vmem<0>();
+    }
+    consume(d0, kt0, vt0, qp0);
+    if (!more) break;
+
+    more = to_issue > 0;
+    if (more) {
+      d0 = describe(cur, next_entry);
+      if (d0.q_start) {
+        qpar ^= 1;
+        issue_query(d0, qs[qpar]);
+      }
+      qp0 = qpar;
+      issue_tile(d0, kt0, vt0);
+      if (--to_issue > 0) {
+        advance(cur);
+        next_entry = table_entry(cur);
+      }
+      wait_vmem<2 * S::LOADS>();
+    } else {
+      wait_vmem<0>();
+    }
+    consume(d1, kt1, vt1, qp1);
+    if (!more) break;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Merge of the units that span workgroups
+// ---------------------------------------------------------------------------
+struct StreamMergeArgs {
+  const float* part_o;
+  const float* part_ml;
+  const float* unit_span;
+  const int32_t* row_map;
+  int32_t group, head_groups, heads_per_group, units_per_row, wgs;
+  uint16_t* out;
+  int64_t out_stride;
+};
+
+// One wave per (row, query head).
+template <int D>
+__global__ __launch_bounds__(64) void stream_merge_kernel(StreamMergeArgs m) {
+  constexpr int PER_LANE = D / 64;
+  const int lane = threadIdx.x;
+  const int head = blockIdx.x, row = blockIdx.y;
+  const int kvh = head / m.group, within = head - kvh * m.group;
+  const int hg = within / 16, hh = within - hg * 16;
+  const int64_t unit = (int64_t)row * m.units_per_row + kvh * m.head_groups + hg;
+  const int first_slot = __float_as_int(m.unit_span[unit * 2]);
+  const int w_last = __float_as_int(m.unit_span[unit * 2 + 1]);
+  const int w_first = first_slot >> 1;
+  if (w_first >= w_last) return;            // finalised by its only workgroup
+  if (first_slot < 0 || w_last >= m.wgs) return;  // not a span this call wrote
+  const int nslots = w_last - w_first + 1;
+  auto slot_of_part = [&](int k) { return k == 0 ? first_slot : 2 * (w_first + k); };
+  float mm = -INFINITY;
+  for (int k = 0; k < nslots; ++k)
+    mm = fmaxf(mm, m.part_ml[((int64_t)slot_of_part(k) * m.heads_per_group + hh) * 2]);
+  float acc[PER_LANE];
+#pragma unroll
+  for (int e = 0; e < PER_LANE; ++e) acc[e] = 0.f;
+  float ll = 0.f;
+  for (int k = 0; k < nslots; ++k) {
+    const int64_t pi = (int64_t)slot_of_part(k) * m.heads_per_group + hh;
+    const float mp = m.part_ml[pi * 2];
+    const float sc = mp == -INFINITY ? 0.f : fast_exp2(mp - mm);
+    ll += sc * m.part_ml[pi * 2 + 1];
+#pragma unroll
+    for (int e = 0; e < PER_LANE; ++e) acc[e] += sc * m.part_o[pi * D + lane + 64 * e];
+  }
+  const float inv = ll > 0.f ? 1.f / ll : 0.f;
+  const int orow = m.row_map ? m.row_map[row] : row;
+  uint16_t* dst = m.out + (int64_t)orow * m.out_stride + (int64_t)head * D;
+#pragma unroll
+  for (int e = 0; e < PER_LANE; ++e) dst[lane + 64 * e] = (uint16_t)bf16_bits(acc[e] * inv);
+}
+
+template <int D, bool SOFTCAP>
+int resident_per_cu() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<D, SOFTCAP>, 64, 0) != hipSuccess ||
+      n <= 0)
+    n = 1;
+  return n;
+}
+
+template <int D>
+int resident_per_cu(bool softcap) {
+  return softcap ? resident_per_cu<D, true>() : resident_per_cu<D, false>();
+}
+
+}  // namespace
+
+int device_cus();
+
+// Workgroups of the balanced grid: the CUs times the workgroups one CU keeps
+// resident (LDS-bound), queried once per device and kernel variant.
+int stream_decode_wgs(int head_dim, bool softcap) {
+  static std::mutex mu;
+  static int cached[64][3][2] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  const int di = head_dim == 64 ? 0 : (head_dim == 128 ? 1 : 2);
+  std::lock_guard<std::mutex> lock(mu);
+  int& slot = cached[dev][di][softcap ? 1 : 0];
+  if (!slot) {
+    int per_cu = 1;
+    switch (head_dim) {
+      case 64: per_cu = resident_per_cu<64>(softcap); break;
+      case 128: per_cu = resident_per_cu<128>(softcap); break;
+      default: per_cu = resident_per_cu<256>(softcap); break;
+    }
+    slot = device_cus() * per_cu;
+  }
+  return slot;
+}
+
+size_t stream_decode_workspace_bytes(int head_dim, int heads_per_group, int64_t units, int wgs) {
+  const size_t parts = (size_t)2 * wgs * heads_per_group;
+  const size_t o_bytes = (parts * head_dim * sizeof(float) + 255) & ~size_t{255};
+  const size_t ml_bytes = (parts * 2 * sizeof(float) + 255) & ~size_t{255};
+  return o_bytes + ml_bytes + (size_t)units * 2 * sizeof(float);
+}
+
+int launch_stream_decode(const DecodeArgs& a, bool softcap, int head_dim, int wgs, void* workspace,
+                         hipStream_t stream) {
+  StreamArgs sa{};
+  sa.d = a;
+  sa.units_per_row = a.kv_heads * a.head_groups;
+  sa.wgs = wgs;
+  const size_t parts = (size_t)2 * wgs * a.heads_per_group;
+  const size_t o_bytes = (parts * head_dim * sizeof(float) + 255) & ~size_t{255};
+  const size_t ml_bytes = (parts * 2 * sizeof(float) + 255) & ~size_t{255};
+  sa.d.part_o = static_cast<float*>(workspace);
+  sa.d.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes);
+  sa.unit_span = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes + ml_bytes);
+
+  const dim3 grid(wgs);
+#define GK_STREAM_LAUNCH(D)                                                                      \
+  if (softcap) decode_stream_kernel<D, true><<<grid, 64, 0, stream>>>(sa);                       \
+  else decode_stream_kernel<D, false><<<grid, 64, 0, stream>>>(sa);
+  switch (head_dim) {
+    case 64: GK_STREAM_LAUNCH(64) break;
+    case 128: GK_STREAM_LAUNCH(128) break;
+    default: GK_STREAM_LAUNCH(256) break;
+  }
+#undef GK_STREAM_LAUNCH
+  if (int rc = hip_status(hipGetLastError(), "gk_paged_decode stream launch")) return rc;
+
+  StreamMergeArgs m{};
+  m.part_o = sa.d.part_o;
+  m.part_ml = sa.d.part_ml;
+  m.unit_span = sa.unit_span;
+  m.row_map = a.row_map;
+  m.group = a.group;
+  m.head_groups = a.head_groups;
+  m.heads_per_group = a.heads_per_group;
+  m.units_per_row = sa.units_per_row;
+  m.wgs = wgs;
+  m.out = a.out;
+  m.out_stride = a.out_stride;
+  const dim3 mgrid(a.q_heads, a.rows);
+  switch (head_dim) {
+    case 64: stream_merge_kernel<64><<<mgrid, 64, 0, stream>>>(m); break;
+    case 128: stream_merge_kernel<128><<<mgrid, 64, 0, stream>>>(m); break;
+    default: stream_merge_kernel<256><<<mgrid, 64, 0, stream>>>(m); break;
+  }
+  return hip_status(hipGetLastError(), "gk_paged_decode stream merge launch");
+}
+
+}  // namespace gk

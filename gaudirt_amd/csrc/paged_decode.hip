@@ -35,7 +35,7 @@
 // q.k times scale; probabilities are rounded to bf16 before P.V as in the
 // reference, but relative to a running rather than the final max, and
 // normalised once at the end; sums use the unrounded fp32 probabilities.
-#include "gk_mfma.hpp"
+#include "decode_common.hpp"
 
 #include <algorithm>
 
@@ -50,38 +50,12 @@ constexpr int kWaves = 4;
 #endif
 template <int D>
 constexpr int mfma_waves_per_simd() { return D == 256 ? 2 : GK_MFMA_WAVES_PER_SIMD; }
-// The MFMA kernel re-bases its running max only when a score exceeds it by more
-// than this (log2 units): probabilities stay <= 2^8 and rescales are rare.
-constexpr float kLazyRescale = 8.f;
 
-struct DecodeArgs {
-  const uint16_t* query;
-  int64_t q_stride;
-  const uint16_t* pool;
-  int64_t slots;
-  const int32_t* block_tables;
-  int64_t bt_stride;
-  int32_t block_shift;
-  const int32_t* row_request;
-  const int32_t* row_context;
-  const int32_t* row_map;
-  int32_t rows, q_heads, kv_heads, group, head_groups, heads_per_group;
-  float score_scale;  // scale * log2(e), or scale / softcap when capping
-  float softcap_log2; // softcap * log2(e) when capping
-  int32_t window, partition, max_parts;
-  uint16_t* out;
-  int64_t out_stride;
-  float* part_o;
-  float* part_ml;
-};
 
 __device__ __forceinline__ uint32_t word(const uint4& v, int e) {
   return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
 }
 
-__device__ __forceinline__ int visible_left(int ctx, int window) {
-  return (window > 0 && ctx > window) ? ctx - window : 0;
-}
 
 // Partition bounds shared by both kernels: keys [t_begin, t_end) of the row.
 struct PartitionRange {
@@ -112,16 +86,6 @@ __device__ __forceinline__ int stage_block_ids(const DecodeArgs& a, const int32_
 // ---------------------------------------------------------------------------
 // MFMA kernel
 // ---------------------------------------------------------------------------
-template <int D>
-struct MfmaShape {
-  static constexpr int TS = D == 256 ? 16 : 32;   // keys per step
-  static constexpr int TG = TS / 16;              // 16-key groups per step (QK tiles)
-  static constexpr int NC = D / 32;               // 32-dim k chunks of Q.K
-  static constexpr int CPR = D / 8;               // 16-byte chunks per head row
-  static constexpr int LOADS = TS * CPR / 64;     // 16-byte loads per lane per tile
-  static constexpr int NO = D / 16;               // 16-dim output chunks of P.V
-  static constexpr int TILE = TS * D * 2;         // bytes of one K or V tile in LDS
-};
 
 // One wave per workgroup; the workgroup owns (partition blockIdx.x, kv head /
 // head group blockIdx.y, query row blockIdx.z). Waves never synchronise with
@@ -262,7 +226,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
       }
     mx = fmaxf(mx, shfl_xor(mx, 16));
     mx = fmaxf(mx, shfl_xor(mx, 32));
-    if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazyRescale)) {
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kDecodeLazyRescale)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
       l_run *= alpha;
@@ -760,8 +724,19 @@ int device_cus() {
 //  - Otherwise 2048-key items while one round of them (at the expected mean
 //    length max_context / 2) fits the resident waves, else 1024.
 // dot2 path: halve a 2048-key partition until the items fill the GPU.
+// The balanced schedule (decode_stream.hip) serves the MFMA path whenever the
+// caller leaves the partition to the library and every TS-key tile lies in one
+// pool block; an explicit partition, small blocks and small groups take the
+// partitioned kernels.
+bool use_stream(const gk_decode_params* p) {
+  const int group = p->q_heads / p->kv_heads;
+  const int ts = p->head_dim == 256 ? 16 : 32;
+  return p->partition_tokens == 0 && use_mfma(group) && p->block_size >= ts;
+}
+
 int32_t decode_partition(const gk_decode_params* p) {
   if (p->partition_tokens > 0) return p->partition_tokens;
+  if (use_stream(p)) return 0;
   const int group = p->q_heads / p->kv_heads;
   const int hpw = heads_per_workgroup(group);
   const int64_t units = (int64_t)p->rows * p->kv_heads * ((group + hpw - 1) / hpw);
@@ -784,10 +759,20 @@ int32_t decode_partition(const gk_decode_params* p) {
 
 int32_t decode_max_parts(const gk_decode_params* p) {
   const int32_t part = decode_partition(p);
+  if (part == 0) return 1;
   return std::max<int32_t>(1, (p->max_context + part - 1) / part);
 }
 
+int64_t stream_units(const gk_decode_params* p) {
+  const int group = p->q_heads / p->kv_heads;
+  const int hpw = heads_per_workgroup(group);
+  return (int64_t)p->rows * p->kv_heads * ((group + hpw - 1) / hpw);
+}
+
 size_t decode_workspace_bytes(const gk_decode_params* p) {
+  if (p->rows > 0 && use_stream(p))
+    return stream_decode_workspace_bytes(p->head_dim, heads_per_workgroup(p->q_heads / p->kv_heads), stream_units(p),
+                                         stream_decode_wgs(p->head_dim, p->softcap > 0.f));
   const int32_t parts = decode_max_parts(p);
   if (parts <= 1 || p->rows == 0) return 0;
   const size_t n = (size_t)p->rows * p->q_heads * parts;
@@ -838,6 +823,8 @@ int paged_decode(const gk_decode_params* p, void* workspace, size_t workspace_by
   a.max_parts = max_parts;
   a.out = static_cast<uint16_t*>(p->out);
   a.out_stride = p->out_row_stride;
+  if (use_stream(p))
+    return launch_stream_decode(a, softcap, p->head_dim, stream_decode_wgs(p->head_dim, softcap), workspace, stream);
   if (need) {
     const size_t n = (size_t)p->rows * p->q_heads * max_parts;
     const size_t o_bytes = (n * p->head_dim * sizeof(float) + 255) & ~size_t{255};

@@ -87,7 +87,10 @@ typedef struct gk_decode_params {
   float softcap;               /* 0 = off */
   int32_t sliding_window;      /* <= 0 = off */
   int32_t max_context;         /* host bound: row_context[r] <= max_context for every row */
-  int32_t partition_tokens;    /* split-K partition (multiple of 32); 0 = library choice */
+  int32_t partition_tokens;    /* split-K partition (multiple of 32); 0 = library choice: for
+                                  GQA groups >= 4 and block_size >= 32 (16 at head_dim 256) a
+                                  balanced split of all key tiles over one resident grid,
+                                  otherwise a partition sized from the batch */
   void* out;                   /* bf16 [rows, out_row_stride] */
   int64_t out_row_stride;      /* elements */
   /* Optional fused KV store of the new token rows (NULL new_key = none): written
@@ -103,7 +106,8 @@ typedef struct gk_decode_params {
 
 /* Workspace bytes gk_paged_decode needs for these parameters (0 if none). */
 size_t gk_paged_decode_workspace_bytes(const gk_decode_params* params);
-/* The split-K partition gk_paged_decode uses for these parameters. */
+/* The split-K partition gk_paged_decode uses for these parameters; 0 when the
+ * balanced split (partitions chosen on the device from row_context) applies. */
 int32_t gk_paged_decode_partition_tokens(const gk_decode_params* params);
 int gk_paged_decode(const gk_decode_params* params, void* workspace, size_t workspace_bytes,
                     hipStream_t stream);
