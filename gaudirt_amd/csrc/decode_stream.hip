@@ -566,20 +566,35 @@ __global__ __launch_bounds__(64) void stream_merge_kernel(StreamMergeArgs m) {
   if (first_slot < 0 || w_last >= m.wgs) return;  // not a span this call wrote
   const int nslots = w_last - w_first + 1;
   auto slot_of_part = [&](int k) { return k == 0 ? first_slot : 2 * (w_first + k); };
-  float mm = -INFINITY;
-  for (int k = 0; k < nslots; ++k)
-    mm = fmaxf(mm, m.part_ml[((int64_t)slot_of_part(k) * m.heads_per_group + hh) * 2]);
+  // One pass with a running max; the partials of four slots are loaded
+  // together, so a unit costs about one memory round trip per four slots.
+  constexpr int BATCH = 4;
+  float mm = -INFINITY, ll = 0.f;
   float acc[PER_LANE];
 #pragma unroll
   for (int e = 0; e < PER_LANE; ++e) acc[e] = 0.f;
-  float ll = 0.f;
-  for (int k = 0; k < nslots; ++k) {
-    const int64_t pi = (int64_t)slot_of_part(k) * m.heads_per_group + hh;
-    const float mp = m.part_ml[pi * 2];
-    const float sc = mp == -INFINITY ? 0.f : fast_exp2(mp - mm);
-    ll += sc * m.part_ml[pi * 2 + 1];
+  for (int k0 = 0; k0 < nslots; k0 += BATCH) {
+    float mp[BATCH], lp[BATCH], op[BATCH][PER_LANE];
 #pragma unroll
-    for (int e = 0; e < PER_LANE; ++e) acc[e] += sc * m.part_o[pi * D + lane + 64 * e];
+    for (int u = 0; u < BATCH; ++u) {
+      const int64_t pi = (int64_t)slot_of_part(min(k0 + u, nslots - 1)) * m.heads_per_group + hh;
+      mp[u] = m.part_ml[pi * 2];
+      lp[u] = m.part_ml[pi * 2 + 1];
+#pragma unroll
+      for (int e = 0; e < PER_LANE; ++e) op[u][e] = m.part_o[pi * D + lane + 64 * e];
+    }
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      // Slots past the unit's last (clamped duplicates) weigh zero.
+      const float mu = k0 + u < nslots ? mp[u] : -INFINITY;
+      const float mn = fmaxf(mm, mu);
+      const float fa = mm == -INFINITY ? 0.f : fast_exp2(mm - mn);
+      const float fb = mu == -INFINITY ? 0.f : fast_exp2(mu - mn);
+      ll = ll * fa + lp[u] * fb;
+#pragma unroll
+      for (int e = 0; e < PER_LANE; ++e) acc[e] = acc[e] * fa + op[u][e] * fb;
+      mm = mn;
+    }
   }
   const float inv = ll > 0.f ? 1.f / ll : 0.f;
   const int orow = m.row_map ? m.row_map[row] : row;
