@@ -58,6 +58,21 @@ def parse_args():
     return ap.parse_args()
 
 
+def measured_traffic(workload):
+    """HBM bytes per launch of the decode kernel, as last measured with rocprofv3 PMC
+    (FETCH_SIZE x2 + WRITE_SIZE) and recorded with its command in
+    profiles/decode_stream_<workload>_traffic.md; None when no measurement exists."""
+    path = os.path.join(ROOT, "profiles", f"decode_stream_{workload}_traffic.md")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(dc, target_seconds):
     """Time the C oracle's direct_bf16_pv (reference restatement) on a bounded sample of the batch."""
     import numpy as np
@@ -250,7 +265,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": measured_traffic(args.workload),
         },
         "cpu_baseline": cpu,
     }
