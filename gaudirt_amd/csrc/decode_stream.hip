@@ -40,26 +40,6 @@ namespace {
 
 typedef __attribute__((address_space(3))) char lds_char_t;
 
-// One 16-byte direct load per lane, HBM -> LDS: lane l's bytes land at LDS
-// address lds + 16 l. Written as an asm statement so that the compiler's
-// wait-count model never sees the LDS side: the kernel orders every read of
-// a stage after that stage's loads with explicit vmcnt waits, and the
-// compiler's own tracking of direct loads (which cannot tell the two stages
-// apart here) would otherwise wait for the other stage's loads as well. M0
-// holds the LDS base; nothing else in this kernel uses M0 (the s_nop covers
-// the M0-write -> direct-load hazard).
-__device__ __forceinline__ void lds_dma16(uint32_t lds, __amdgpu_buffer_rsrc_t rsrc, uint32_t voffset) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds),
-      "v"(voffset), "s"(rsrc)
-      : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const lds_char_t*)p;
-}
 
 struct StreamArgs {
   DecodeArgs d;
@@ -84,12 +64,6 @@ __device__ __forceinline__ RowTiles row_tiles(int ctx, int window) {
   return r;
 }
 
-// Wave-uniform load through the scalar cache (s_load). The data is only read
-// by this kernel; the constant address space tells the compiler so, which it
-// cannot prove itself once LDS direct loads (memory writes) are in the loop.
-__device__ __forceinline__ int32_t scalar_load(const int32_t* p, int64_t i) {
-  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
-}
 
 __device__ __forceinline__ int bperm(int lane_src, int x) { return __builtin_amdgcn_ds_bpermute(lane_src << 2, x); }
 

@@ -61,4 +61,33 @@ __device__ __forceinline__ bf16x4_t lds_read_tr4(const char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)p);
 }
 
+// One 16-byte direct load per lane, HBM -> LDS: lane l's bytes land at LDS
+// address lds + 16 l. Written as an asm statement so that the compiler's
+// wait-count model never sees the LDS side: kernels order every read of a
+// stage after that stage's loads with explicit vmcnt waits (and barriers),
+// while the compiler's own tracking of direct loads either cannot tell two
+// stages apart or waits for every direct load in flight before a barrier. M0
+// holds the LDS base; no other code in these kernels uses M0 (the s_nop covers
+// the M0-write -> direct-load hazard).
+__device__ __forceinline__ void lds_dma16(uint32_t lds, __amdgpu_buffer_rsrc_t rsrc, uint32_t voffset) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds),
+      "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+
+// Wave-uniform load through the scalar cache (s_load). The data is only read
+// by the kernel; the constant address space tells the compiler so, which it
+// cannot prove itself once LDS direct loads (memory writes) are in the loop.
+__device__ __forceinline__ int32_t scalar_load(const int32_t* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
+// LDS byte address of a __shared__ object (or a pointer into one).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
 }  // namespace gk

@@ -31,7 +31,11 @@ namespace gk {
 namespace {
 
 constexpr int kPrefillWaves = 4;
-constexpr int kQrowsPerWave = 32;                          // two 16-column tiles
+// 16-column query tiles per wave. Two, with two workgroups per CU: three or
+// four tiles per wave (one workgroup per CU) measured 2x slower on C4, the
+// barrier waits no longer hidden by a second workgroup.
+constexpr int kNT = 2;
+constexpr int kQrowsPerWave = 16 * kNT;
 constexpr int kQrows = kPrefillWaves * kQrowsPerWave;     // query rows per workgroup
 constexpr int kKeys = 32;                                  // keys per step
 constexpr float kLazyRescale = 8.f;
@@ -49,6 +53,7 @@ struct PrefillArgs {
   const int32_t* seq_rows;
   const int32_t* seq_prefix;
   int32_t q_heads, kv_heads, group, rows_per_tile;
+  int32_t tiles, seqs;  // row tiles per sequence; sequences
   float score_scale;   // scale * log2(e), or scale / softcap when capping
   float softcap_log2;  // softcap * log2(e) when capping
   int32_t window;
@@ -66,18 +71,21 @@ struct PrefillShape {
 };
 
 template <int D, bool SOFTCAP>
-__global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_kernel(PrefillArgs a) {
   using S = PrefillShape<D>;
   __shared__ __attribute__((aligned(16))) char kt0[S::TILE];
   __shared__ __attribute__((aligned(16))) char vt0[S::TILE];
   __shared__ __attribute__((aligned(16))) char kt1[S::TILE];
   __shared__ __attribute__((aligned(16))) char vt1[S::TILE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS bases of the direct loads)
   const int q = lane >> 4, c16 = lane & 15;
-  const int seq = blockIdx.z, kvh = blockIdx.y;
+  // Work item (row tile, kv head, sequence), row tiles fastest.
+  const int item = blockIdx.x;
+  const int tile = item % a.tiles, kvh = (item / a.tiles) % a.kv_heads, seq = item / (a.tiles * a.kv_heads);
   const int rows = a.seq_rows[seq];
-  const int r0 = blockIdx.x * a.rows_per_tile;
+  const int r0 = tile * a.rows_per_tile;
   if (r0 >= rows) return;
   const int nr = min(a.rows_per_tile, rows - r0);
   const int prefix = a.seq_prefix[seq];
@@ -90,12 +98,12 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillA
   const int kb0 = key_begin & ~(kKeys - 1);
   const int nsteps = (key_end - kb0 + kKeys - 1) / kKeys;
 
-  // This lane's two query rows (one per 16-column tile): qrow = (row, head).
-  int qpos[2], qleft[2];
-  bool qvalid[2];
-  bf16x8_t qb[2][S::NC];
+  // This lane's query rows (one per 16-column tile): qrow = (row, head).
+  int qpos[kNT], qleft[kNT];
+  bool qvalid[kNT];
+  bf16x8_t qb[kNT][S::NC];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < kNT; ++nt) {
     const int qr = wave * kQrowsPerWave + nt * 16 + c16;
     const int row = qr / g, head = qr % g;
     qvalid[nt] = row < nr;
@@ -110,12 +118,20 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillA
     }
   }
 
-  f32x4_t o[2][S::NO];
+  // Smallest query position and largest window start over this wave's valid rows.
+  const int wave_pos_min = pos_lo + (wave * kQrowsPerWave) / g;
+  const int wave_left_max =
+      a.window > 0 ? pos_lo + min(nr - 1, (wave * kQrowsPerWave + kQrowsPerWave - 1) / g) - a.window + 1 : 0;
+
+  f32x4_t o[kNT][S::NO];
+  float m_run[kNT], l_run[kNT];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
+  for (int nt = 0; nt < kNT; ++nt) {
 #pragma unroll
     for (int c = 0; c < S::NO; ++c) o[nt][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+  }
 
   const uint16_t* kbase = a.pool + (int64_t)kvh * a.slots * D;
   const uint16_t* vbase = kbase + (int64_t)a.kv_heads * a.slots * D;
@@ -129,21 +145,22 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillA
   // consecutive from the block's slot for tb (one scalar block-table read).
   // Piece p = 64 (LOADS * wave + i) + lane: token p / CPR, stored chunk
   // p % CPR holding the token's chunk (p % CPR) ^ swz(token).
-  auto issue = [&](int tb, char* kt, char* vt) {
-    const uint32_t row0 = (uint32_t)((bt[tb >> shift] << shift) | (tb & bmask)) * (2 * D);
+  auto issue = [&](int tb, int entry, char* kt, char* vt) {
+    const uint32_t row0 = (uint32_t)((entry << shift) | (tb & bmask)) * (2 * D);
+    const uint32_t kl = lds_addr(kt), vl = lds_addr(vt);
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int p = (S::LOADS * wave + i) * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + (S::LOADS * wave + i) * 1024), 16,
-                                               row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4), 0, 0, 0);
+      lds_dma16(kl + (S::LOADS * wave + i) * 1024, krs, row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4));
     }
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int p = (S::LOADS * wave + i) * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + (S::LOADS * wave + i) * 1024), 16,
-                                               row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4), 0, 0, 0);
+      lds_dma16(vl + (S::LOADS * wave + i) * 1024, vrs, row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4));
     }
   };
+  // Block-table entry of the step at key tb (scalar load, fetched a step ahead).
+  auto entry_of = [&](int tb) { return scalar_load(bt, tb >> shift); };
 
   auto consume = [&](int tb, const char* kt, char* vt) {
     if (tb + kKeys > key_end) {
@@ -154,7 +171,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillA
       __syncthreads();
     }
     // S^T = K.Q^T: lane (q, c16) gets qrow c16 (+16 nt), keys tb + 16h + 4q + r.
-    f32x4_t sc[2][2];
+    f32x4_t sc[2][kNT];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int tt = 16 * h + c16;
@@ -163,29 +180,42 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillA
       for (int c = 0; c < S::NC; ++c)
         kr[c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt)) << 4));
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < kNT; ++nt) {
         sc[h][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < S::NC; ++c) sc[h][nt] = mfma32(kr[c], qb[nt][c], sc[h][nt]);
       }
     }
 
-    bf16x8_t pa[2];
+    // A step whose keys every valid query row of this wave sees (below the
+    // causal diagonal, inside the window) needs no per-element mask, and its
+    // scale folds into the exponent (max of raw scores times scale > 0, then
+    // exp2(fma(s, scale, -max))): a third of the softmax instructions.
+    const bool full = !SOFTCAP && tb + kKeys - 1 <= wave_pos_min && tb >= wave_left_max;
+    bf16x8_t pa[kNT];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < kNT; ++nt) {
       float mx = -INFINITY;
+      if (full) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = tb + 16 * h + 4 * q + r;
-          float s;
-          if constexpr (SOFTCAP) s = a.softcap_log2 * soft_tanh(sc[h][nt][r] * a.score_scale);
-          else s = sc[h][nt][r] * a.score_scale;
-          s = (key <= qpos[nt] && key >= qleft[nt]) ? s : -INFINITY;
-          sc[h][nt][r] = s;
-          mx = fmaxf(mx, s);
-        }
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[h][nt][r]);
+        mx *= a.score_scale;
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = tb + 16 * h + 4 * q + r;
+            float s;
+            if constexpr (SOFTCAP) s = a.softcap_log2 * soft_tanh(sc[h][nt][r] * a.score_scale);
+            else s = sc[h][nt][r] * a.score_scale;
+            s = (key <= qpos[nt] && key >= qleft[nt]) ? s : -INFINITY;
+            sc[h][nt][r] = s;
+            mx = fmaxf(mx, s);
+          }
+      }
       mx = fmaxf(mx, shfl_xor(mx, 16));
       mx = fmaxf(mx, shfl_xor(mx, 32));
       if (__builtin_amdgcn_ballot_w64(mx > m_run[nt] + kLazyRescale)) {
@@ -206,7 +236,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillA
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = fast_exp2(sc[h][nt][r] - base);
+          const float p = full ? fast_exp2(__builtin_fmaf(sc[h][nt][r], a.score_scale, -base))
+                               : fast_exp2(sc[h][nt][r] - base);
           l_run[nt] += p;
           pa[nt][4 * h + r] = (__bf16)p;
         }
@@ -222,44 +253,41 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 2) void prefill_kernel(PrefillA
       const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1)) << 4) + ((c16 & 1) << 3));
       const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) o[nt][c] = mfma32(pa[nt], vb, o[nt][c]);
+      for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[nt], vb, o[nt][c]);
     }
   };
 
-  // Two-stage pipeline over the workgroup: the next tile's loads are in flight
-  // while the current one is attended. Barriers: (1) every wave's loads of the
-  // current stage have landed, (2) every wave is done with a stage before it
-  // is refilled.
+  // Two-stage pipeline over the workgroup, one barrier per step: after it,
+  // every wave's loads of the current stage have landed (each waited for its
+  // own, the only ones in flight) and every wave has finished the previous
+  // step, so the other stage is refilled while this one is attended.
   int tb = kb0;
-  issue(tb, kt0, vt0);
+  issue(tb, entry_of(tb), kt0, vt0);
+  int e_next = nsteps > 1 ? entry_of(tb + kKeys) : 0;
   for (int step = 0; step < nsteps; step += 2) {
+    wait_vmem<0>();
+    __syncthreads();
     const bool more1 = step + 1 < nsteps;
     if (more1) {
-      issue(tb + kKeys, kt1, vt1);
-      wait_vmem<2 * S::LOADS>();
-    } else {
-      wait_vmem<0>();
+      issue(tb + kKeys, e_next, kt1, vt1);
+      if (step + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
     }
-    __syncthreads();
     consume(tb, kt0, vt0);
-    __syncthreads();
     if (!more1) break;
+    wait_vmem<0>();
+    __syncthreads();
     const bool more2 = step + 2 < nsteps;
     if (more2) {
-      issue(tb + 2 * kKeys, kt0, vt0);
-      wait_vmem<2 * S::LOADS>();
-    } else {
-      wait_vmem<0>();
+      issue(tb + 2 * kKeys, e_next, kt0, vt0);
+      if (step + 3 < nsteps) e_next = entry_of(tb + 3 * kKeys);
     }
-    __syncthreads();
     consume(tb + kKeys, kt1, vt1);
-    __syncthreads();
     tb += 2 * kKeys;
   }
 
   // Per-qrow sums over the four lane groups, then normalise and store.
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < kNT; ++nt) {
     float l = l_run[nt];
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
@@ -326,14 +354,17 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
   a.kv_heads = p->kv_heads;
   a.group = p->q_heads / p->kv_heads;
   a.rows_per_tile = kQrows / a.group;
+  a.tiles = (p->max_rows + a.rows_per_tile - 1) / a.rows_per_tile;
+  a.seqs = p->seqs;
   const bool softcap = p->softcap > 0.f;
   a.score_scale = softcap ? p->scale / p->softcap : p->scale * kLog2e;
   a.softcap_log2 = p->softcap * kLog2e;
   a.window = p->sliding_window > 0 ? p->sliding_window : 0;
   a.out = static_cast<uint16_t*>(p->out);
   a.out_stride = p->out_row_stride;
-  const dim3 grid((p->max_rows + a.rows_per_tile - 1) / a.rows_per_tile, p->kv_heads, p->seqs);
-  if (grid.x > 65535u * 1024u) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: too many rows");
+  const int64_t items = (int64_t)a.tiles * p->kv_heads * p->seqs;
+  if (items > (int64_t)1 << 30) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: too many rows");
+  const dim3 grid((unsigned)items);
   if (p->head_dim == 64) launch<64>(a, softcap, grid, stream);
   else launch<128>(a, softcap, grid, stream);
   return hip_status(hipGetLastError(), "gk_paged_prefill launch");
