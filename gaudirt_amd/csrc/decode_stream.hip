@@ -260,12 +260,12 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
-      lds_dma16(kl + i * 1024, krs, t.row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4));
+      lds_dma16(kl + i * 1024, krs, t.row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4));
     }
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
-      lds_dma16(vl + i * 1024, vrs, t.row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4));
+      lds_dma16(vl + i * 1024, vrs, t.row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4));
     }
   };
   // The unit's query heads -> LDS ([head][D], row-major). The resource covers
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       const int tt = 16 * h + c16;
 #pragma unroll
       for (int c = 0; c < S::NC; ++c)
-        kr[h][c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt)) << 4));
+        kr[h][c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt, D / 8)) << 4));
     }
     f32x4_t sc[S::TG];
 #pragma unroll
@@ -430,8 +430,8 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       for (int c = 0; c < S::NO; ++c) {
         const int lc = 2 * c + ((c16 & 3) >> 1);
         const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
-        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
-        const char* p1 = vt + t1 * (2 * D) + ((lc ^ swz(t1)) << 4) + ((c16 & 1) << 3);
+        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3);
+        const char* p1 = vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3);
         const bf16x4_t v0 = lds_read_tr4(p0);
         const bf16x4_t v1 = lds_read_tr4(p1);
         const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -445,7 +445,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       for (int c = 0; c < S::NO; ++c) {
         const int lc = 2 * c + ((c16 & 3) >> 1);
         const int t0 = 4 * q + (c16 >> 2);
-        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
+        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3);
         o[c] = mfma16(pa, lds_read_tr4(p0), o[c]);
       }
     }

@@ -31,11 +31,22 @@ __device__ __forceinline__ int slot_of(const int32_t* s_bt, int b0, int shift, i
 }
 
 // Token swizzle of 16-byte chunks inside an LDS row of a K or V tile: chunk c
-// of token t is stored at c ^ swz(t). Conflict-free both for the row-major
-// tile writes and for the 16-key operand reads (8 consecutive tokens map to 8
-// distinct chunk slots) and the transposed 4-token reads of P.V (4 consecutive
-// tokens map to distinct 32-byte pairs).
-__device__ __forceinline__ int swz(int t) { return ((t & 3) << 1) | ((t >> 2) & 1); }
+// of token t is stored at c ^ swz(t, CPR) (CPR = 16-byte chunks per row).
+// gfx950's LDS serves 256 bytes per clock (64 banks), so a row of d >= 128
+// bf16 starts every 256 bytes at bank 0 and the swizzle has to spread:
+//  - the 16-key operand reads (16 lanes, 16 consecutive tokens, one logical
+//    chunk each): 16 distinct chunk slots;
+//  - the transposed 4-token reads of P.V (32 lanes, 8 consecutive tokens, an
+//    aligned pair of chunks each): 8 distinct pair slots.
+// swz = ((t & 7) << 1) | ((t >> 3) & 1) does both. With d = 64 (8 chunks, two
+// rows per 256 bytes) the 3-bit form ((t & 3) << 1) | ((t >> 2) & 1) keeps the
+// chunk inside the row.
+// (cpr is a compile-time constant at every call site, written D / 8: passing a
+// static member such as MfmaShape<D>::CPR from a lambda inside a kernel template
+// makes the host pass of hipcc drop the kernel's launch stub.)
+__device__ __forceinline__ int swz(int t, int cpr) {
+  return cpr >= 16 ? (((t & 7) << 1) | ((t >> 3) & 1)) : (((t & 3) << 1) | ((t >> 2) & 1));
+}
 
 // Wait until at most N vector memory operations of this wave are outstanding.
 template <int N>

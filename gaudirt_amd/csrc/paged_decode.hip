@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
   auto issue = [&](int tb, char* kt, char* vt) {
     // K and V tiles -> LDS with 16-byte direct loads (global_load_lds_dwordx4):
     // load i, lane l fills piece s = 64 i + l of the tile, i.e. token s / CPR,
-    // stored chunk s % CPR, which holds the token's chunk (s % CPR) ^ swz(token).
+    // stored chunk s % CPR, which holds the token's chunk (s % CPR) ^ swz(token, D / 8).
     // One load instruction thus covers whole 128-byte lines of four keys. When
     // the whole step lies in one pool block (block_size >= TS, the common case)
     // its slots are consecutive and one lookup serves every key; otherwise each
@@ -164,27 +164,27 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
       for (int i = 0; i < S::LOADS; ++i) {
         const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + i * 1024), 16,
-                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4), 0, 0, 0);
+                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4), 0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < S::LOADS; ++i) {
         const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + i * 1024), 16,
-                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4), 0, 0, 0);
+                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4), 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < S::LOADS; ++i) {
         const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
         const uint32_t row = (uint32_t)slot_of(s_bt, b0, shift, min(tb + tt, t_last)) * (2 * D);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + i * 1024), 16, row + ((pc ^ swz(tt)) << 4),
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + i * 1024), 16, row + ((pc ^ swz(tt, D / 8)) << 4),
                                                  0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < S::LOADS; ++i) {
         const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
         const uint32_t row = (uint32_t)slot_of(s_bt, b0, shift, min(tb + tt, t_last)) * (2 * D);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + i * 1024), 16, row + ((pc ^ swz(tt)) << 4),
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + i * 1024), 16, row + ((pc ^ swz(tt, D / 8)) << 4),
                                                  0, 0, 0);
       }
     }
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
       const int tt = 16 * h + c16;
 #pragma unroll
       for (int c = 0; c < S::NC; ++c)
-        kr[h][c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt)) << 4));
+        kr[h][c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt, D / 8)) << 4));
     }
 
     // S^T = K.Q^T: lane (q, c16) gets head c16, tokens tb + 16h + 4q + r.
@@ -272,8 +272,8 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
         // tokens 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2); dims 16c + 4 (c16 & 3)
         const int lc = 2 * c + ((c16 & 3) >> 1);
         const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
-        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
-        const char* p1 = vt + t1 * (2 * D) + ((lc ^ swz(t1)) << 4) + ((c16 & 1) << 3);
+        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3);
+        const char* p1 = vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3);
         const bf16x4_t v0 = lds_read_tr4(p0);
         const bf16x4_t v1 = lds_read_tr4(p1);
         const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
       for (int c = 0; c < S::NO; ++c) {
         const int lc = 2 * c + ((c16 & 3) >> 1);
         const int t0 = 4 * q + (c16 >> 2);
-        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3);
+        const char* p0 = vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3);
         const bf16x4_t v0 = lds_read_tr4(p0);
         o[c] = mfma16(pa, v0, o[c]);
       }

@@ -30,6 +30,8 @@
 namespace gk {
 namespace {
 
+// Waves per workgroup (each owns 16 * kNT query rows). Eight waves (half the
+// K/V re-reads) measured 2% slower on C4 than four.
 constexpr int kPrefillWaves = 4;
 // 16-column query tiles per wave. Two, with two workgroups per CU: three or
 // four tiles per wave (one workgroup per CU) measured 2x slower on C4, the
@@ -38,6 +40,10 @@ constexpr int kNT = 2;
 constexpr int kQrowsPerWave = 16 * kNT;
 constexpr int kQrows = kPrefillWaves * kQrowsPerWave;     // query rows per workgroup
 constexpr int kKeys = 32;                                  // keys per step
+// K/V pipeline depth. Two: three and four stages measured the same on C4 (the
+// kernel is bound by its instruction stream, not by load latency).
+constexpr int kStages = 2;
+static_assert(kStages >= 2 && kStages <= 4, "wait counts cover up to two stages in flight");
 constexpr float kLazyRescale = 8.f;
 
 struct PrefillArgs {
@@ -67,16 +73,16 @@ struct PrefillShape {
   static constexpr int CPR = D / 8;                 // 16-byte chunks per head row
   static constexpr int NO = D / 16;                 // 16-dim output chunks
   static constexpr int TILE = kKeys * D * 2;        // bytes of one K or V tile
-  static constexpr int LOADS = TILE / (kPrefillWaves * 64 * 16);  // per thread per tile
+  static constexpr int NI = TILE / 1024;            // 1 KiB load instructions per tile
 };
 
 template <int D, bool SOFTCAP>
 __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_kernel(PrefillArgs a) {
   using S = PrefillShape<D>;
-  __shared__ __attribute__((aligned(16))) char kt0[S::TILE];
-  __shared__ __attribute__((aligned(16))) char vt0[S::TILE];
-  __shared__ __attribute__((aligned(16))) char kt1[S::TILE];
-  __shared__ __attribute__((aligned(16))) char vt1[S::TILE];
+  // kStages K/V stages. The direct loads are asm statements the compiler does
+  // not track, so one array serves every stage; reads are ordered by the
+  // explicit vmcnt wait and the barrier of each step.
+  __shared__ __attribute__((aligned(16))) char kv[kStages][2][S::TILE];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS bases of the direct loads)
@@ -144,19 +150,18 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   // and blocks hold >= 32 keys, so a step lies in one block: its slots are
   // consecutive from the block's slot for tb (one scalar block-table read).
   // Piece p = 64 (LOADS * wave + i) + lane: token p / CPR, stored chunk
-  // p % CPR holding the token's chunk (p % CPR) ^ swz(token).
+  // p % CPR holding the token's chunk (p % CPR) ^ swz(token, D / 8).
   auto issue = [&](int tb, int entry, char* kt, char* vt) {
     const uint32_t row0 = (uint32_t)((entry << shift) | (tb & bmask)) * (2 * D);
     const uint32_t kl = lds_addr(kt), vl = lds_addr(vt);
+    // Load instruction ins (wave ins % waves) fills 1 KiB piece ins of a tile.
 #pragma unroll
-    for (int i = 0; i < S::LOADS; ++i) {
-      const int p = (S::LOADS * wave + i) * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
-      lds_dma16(kl + (S::LOADS * wave + i) * 1024, krs, row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4));
-    }
-#pragma unroll
-    for (int i = 0; i < S::LOADS; ++i) {
-      const int p = (S::LOADS * wave + i) * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
-      lds_dma16(vl + (S::LOADS * wave + i) * 1024, vrs, row0 + tt * (2 * D) + ((pc ^ swz(tt)) << 4));
+    for (int k = 0; k < (S::NI + kPrefillWaves - 1) / kPrefillWaves; ++k) {
+      const int ins = wave + k * kPrefillWaves;
+      if (ins >= S::NI) break;
+      const int p = ins * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
+      lds_dma16(kl + ins * 1024, krs, row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4));
+      lds_dma16(vl + ins * 1024, vrs, row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4));
     }
   };
   // Block-table entry of the step at key tb (scalar load, fetched a step ahead).
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       bf16x8_t kr[S::NC];
 #pragma unroll
       for (int c = 0; c < S::NC; ++c)
-        kr[c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt)) << 4));
+        kr[c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt, D / 8)) << 4));
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt) {
         sc[h][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -232,15 +237,19 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
         }
       }
       const float base = m_run[nt] == -INFINITY ? 0.f : m_run[nt];
+      float ps[8];
+      if (full) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+        for (int i = 0; i < 8; ++i) ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
+      } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = full ? fast_exp2(__builtin_fmaf(sc[h][nt][r], a.score_scale, -base))
-                               : fast_exp2(sc[h][nt][r] - base);
-          l_run[nt] += p;
-          pa[nt][4 * h + r] = (__bf16)p;
-        }
+        for (int i = 0; i < 8; ++i) ps[i] = fast_exp2(sc[i >> 2][nt][i & 3] - base);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        l_run[nt] += ps[i];
+        pa[nt][i] = (__bf16)ps[i];
+      }
     }
 
     // O[qrow][dim] += P . V: keys 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2),
@@ -249,40 +258,41 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
     for (int c = 0; c < S::NO; ++c) {
       const int lc = 2 * c + ((c16 & 3) >> 1);
       const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
-      const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0)) << 4) + ((c16 & 1) << 3));
-      const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1)) << 4) + ((c16 & 1) << 3));
+      const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3));
+      const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3));
       const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[nt], vb, o[nt][c]);
     }
   };
 
-  // Two-stage pipeline over the workgroup, one barrier per step: after it,
-  // every wave's loads of the current stage have landed (each waited for its
-  // own, the only ones in flight) and every wave has finished the previous
-  // step, so the other stage is refilled while this one is attended.
-  int tb = kb0;
-  issue(tb, entry_of(tb), kt0, vt0);
-  int e_next = nsteps > 1 ? entry_of(tb + kKeys) : 0;
-  for (int step = 0; step < nsteps; step += 2) {
-    wait_vmem<0>();
+  // kStages-deep pipeline over the workgroup, one barrier per step: before it
+  // each wave waits for its own loads of the current stage (the younger ones,
+  // of the next kStages - 2 stages, stay in flight); after it every wave's
+  // loads of the stage have landed and every wave has finished the previous
+  // step, whose buffer is refilled with the step kStages - 1 ahead.
+  constexpr int LPS = 2 * S::NI / kPrefillWaves;  // direct loads per wave per stage
+  static_assert(S::NI % kPrefillWaves == 0, "tile pieces split evenly over the waves");
+  int e_next = 0;
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st) {
+    if (st < nsteps) issue(kb0 + st * kKeys, entry_of(kb0 + st * kKeys), kv[st][0], kv[st][1]);
+  }
+  if (kStages - 1 < nsteps) e_next = entry_of(kb0 + (kStages - 1) * kKeys);
+  for (int step = 0; step < nsteps; ++step) {
+    const int later = min(kStages - 2, nsteps - 1 - step);  // stages in flight beyond this one
+    if (later >= 2) wait_vmem<2 * LPS>();
+    else if (later == 1) wait_vmem<LPS>();
+    else wait_vmem<0>();
     __syncthreads();
-    const bool more1 = step + 1 < nsteps;
-    if (more1) {
-      issue(tb + kKeys, e_next, kt1, vt1);
-      if (step + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
+    const int ahead = step + kStages - 1;
+    if (ahead < nsteps) {
+      const int buf = ahead % kStages;
+      issue(kb0 + ahead * kKeys, e_next, kv[buf][0], kv[buf][1]);
+      if (ahead + 1 < nsteps) e_next = entry_of(kb0 + (ahead + 1) * kKeys);
     }
-    consume(tb, kt0, vt0);
-    if (!more1) break;
-    wait_vmem<0>();
-    __syncthreads();
-    const bool more2 = step + 2 < nsteps;
-    if (more2) {
-      issue(tb + 2 * kKeys, e_next, kt0, vt0);
-      if (step + 3 < nsteps) e_next = entry_of(tb + 3 * kKeys);
-    }
-    consume(tb + kKeys, kt1, vt1);
-    tb += 2 * kKeys;
+    const int cur = step % kStages;
+    consume(kb0 + step * kKeys, kv[cur][0], kv[cur][1]);
   }
 
   // Per-qrow sums over the four lane groups, then normalise and store.
