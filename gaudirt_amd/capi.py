@@ -26,6 +26,8 @@ EXPORTED = [
     "gk_last_error", "gk_version", "gk_kv_store", "gk_paged_decode_workspace_bytes",
     "gk_paged_decode_partition_tokens", "gk_paged_decode", "gk_paged_prefill", "gk_split_k_merge",
     "gk_attn_tile_indices", "gk_advance_decode_lengths",
+    "gk_metadata_workspace_bytes", "gk_metadata_normalize", "gk_block_tables",
+    "gk_paged_alloc_slots", "gk_paged_release_workspace_bytes", "gk_paged_release_slots",
     "gk_allocator_create", "gk_allocator_destroy", "gk_allocator_alloc", "gk_allocator_record_stream",
     "gk_allocator_free", "gk_allocator_empty_cache", "gk_allocator_get_stats",
 ]
@@ -74,6 +76,22 @@ class PrefillParams(_Sized):
     ]
 
 
+class MetadataParams(_Sized):
+    _fields_ = [
+        ("struct_size", ctypes.c_size_t),
+        ("locations", c_void_p), ("batch_requests", c_void_p), ("positions", c_void_p), ("token_ids", c_void_p),
+        ("locations_int64", c_i32), ("requests_int64", c_i32), ("positions_int64", c_i32), ("tokens_int64", c_i32),
+        ("mapping", c_void_p),
+        ("row_seq", c_void_p), ("seq_prefix", c_void_p), ("seq_first_row", c_void_p), ("seq_visible", c_void_p),
+        ("visible_total", c_i64),
+        ("rows", c_i32), ("padded_rows", c_i32), ("batch", c_i32), ("requests", c_i32), ("context", c_i32),
+        ("vocabulary", c_i32),
+        ("slots", c_i64),
+        ("out_locations", c_void_p), ("out_requests", c_void_p), ("out_positions", c_void_p),
+        ("out_tokens", c_void_p), ("status", c_void_p), ("token_status", c_void_p), ("page_flags", c_void_p),
+    ]
+
+
 class AllocatorStats(ctypes.Structure):
     _fields_ = [(name, ctypes.c_uint64) for name in (
         "allocated_bytes", "peak_bytes", "reserved_bytes", "largest_free_block", "slabs", "events_created")]
@@ -110,6 +128,15 @@ def load():
                                      c_void_p]
     lib.gk_attn_tile_indices.argtypes = [c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p]
     lib.gk_advance_decode_lengths.argtypes = [c_void_p, c_void_p, c_i64, c_void_p, c_void_p, c_void_p]
+    lib.gk_metadata_workspace_bytes.restype = ctypes.c_size_t
+    lib.gk_metadata_workspace_bytes.argtypes = [c_i32, c_i32]
+    lib.gk_metadata_normalize.argtypes = [ctypes.POINTER(MetadataParams), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.gk_block_tables.argtypes = [c_void_p, c_i32, c_i32, c_i32, c_void_p, c_i32, c_void_p]
+    lib.gk_paged_alloc_slots.argtypes = [c_void_p, c_void_p, c_void_p, c_i32, c_i64, c_i64, c_void_p, c_void_p]
+    lib.gk_paged_release_workspace_bytes.restype = ctypes.c_size_t
+    lib.gk_paged_release_workspace_bytes.argtypes = [c_i64]
+    lib.gk_paged_release_slots.argtypes = [c_void_p, c_i64, c_i64, c_i64, c_void_p, ctypes.c_size_t, c_void_p,
+                                           c_void_p, c_void_p]
     lib.gk_allocator_create.argtypes = [c_i32, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(c_void_p)]
     lib.gk_allocator_destroy.argtypes = [c_void_p]
     lib.gk_allocator_alloc.argtypes = [c_void_p, ctypes.c_uint64, c_void_p, ctypes.POINTER(c_void_p)]

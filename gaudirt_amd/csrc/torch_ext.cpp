@@ -7,6 +7,7 @@
 //   torch.ops.gaudirt._paged_attn_validated
 //   torch.ops.gaudirt._advance_decode_lengths
 //   gaudirt_amd._C._allocate_paged_kv     head-major pool on the block allocator
+//   gaudirt_amd._C._allocate_paged_slots / _release_paged_slots   page allocator
 //
 // Errors are TORCH_CHECK failures (RuntimeError in Python) raised before any
 // KV byte is written, with the message fragments the reference's tests match.
@@ -50,6 +51,27 @@ int current_device() {
 
 at::TensorOptions device_int32() {
   return at::TensorOptions().device(at::Device(at::kCUDA, current_device())).dtype(at::kInt);
+}
+
+// Host words -> a device int32 tensor of `total` words (the first
+// words.size() filled) on the current stream through pinned staging: the
+// host does not wait for queued device work, and torch's host allocator
+// keeps the staging block until the copy has run.
+at::Tensor upload_words(const std::vector<int32_t>& words, int64_t total) {
+  auto device = at::empty({total}, device_int32());
+  if (!words.empty()) {
+    auto host = at::empty({static_cast<int64_t>(words.size())}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
+    std::memcpy(host.data_ptr<int32_t>(), words.data(), words.size() * sizeof(int32_t));
+    device.narrow(0, 0, static_cast<int64_t>(words.size())).copy_(host, /*non_blocking=*/true);
+  }
+  return device;
+}
+
+// Word offset of the next 256-byte aligned section of a packed int32 buffer.
+int64_t reserve_words(int64_t& cursor, int64_t count) {
+  const int64_t start = cursor;
+  cursor += (count + 63) / 64 * 64;
+  return start;
 }
 
 // ---------------------------------------------------------------------------
@@ -185,8 +207,10 @@ const PlanInfo& plan_data(const at::Tensor& tensor) {
 }
 
 // ---------------------------------------------------------------------------
-// PagedMetadata (src/bridge/paged_metadata.hpp:17-109, host constructor
-// src/bridge/paged_metadata.cpp:82-174).
+// PagedMetadata (src/bridge/paged_metadata.hpp:17-109). Host constructor
+// src/bridge/paged_metadata.cpp:82-174; device constructors (from_device,
+// from_device_with_tokens, _from_scheduler, _from_scheduler_fused)
+// src/bridge/paged_metadata.cpp:176-430.
 // ---------------------------------------------------------------------------
 class PagedMetadata : public torch::CustomClassHolder {
  public:
@@ -257,17 +281,231 @@ class PagedMetadata : public torch::CustomClassHolder {
     slots_ = slots;
     request_count_ = request_count;
     context_ = context;
-    // Device copies for the kernels and for the row accessors.
-    const auto upload = [&](const std::vector<int32_t>& v, std::vector<int64_t> shape) {
-      auto host = at::from_blob(const_cast<int32_t*>(v.data()), shape, at::TensorOptions().dtype(at::kInt));
-      return host.to(device_int32().device(), /*non_blocking=*/false, /*copy=*/true);
+    // One device buffer: header | locations | requests | positions | mapping.
+    int64_t cursor = 0;
+    const auto header_offset = reserve_words(cursor, 1);
+    const auto locations_offset = reserve_words(cursor, m);
+    const auto requests_offset = reserve_words(cursor, m);
+    const auto positions_offset = reserve_words(cursor, m);
+    const auto mapping_offset = reserve_words(cursor, mapping.numel());
+    std::vector<int32_t> words(cursor, 0);
+    words[header_offset] = static_cast<int32_t>(m);
+    std::copy(locations_h_.begin(), locations_h_.end(), words.begin() + locations_offset);
+    std::copy(requests_h_.begin(), requests_h_.end(), words.begin() + requests_offset);
+    std::copy(positions_h_.begin(), positions_h_.end(), words.begin() + positions_offset);
+    std::copy(mapping_h_.begin(), mapping_h_.end(), words.begin() + mapping_offset);
+    storage_ = upload_words(words, cursor);
+    header_ = storage_.narrow(0, header_offset, 1);
+    locations_ = storage_.narrow(0, locations_offset, m);
+    requests_ = storage_.narrow(0, requests_offset, m);
+    positions_ = storage_.narrow(0, positions_offset, m);
+    mapping_ = storage_.narrow(0, mapping_offset, mapping.numel()).view({request_count, context});
+  }
+
+  // Device constructor. Sequence s covers the next lengths[s] rows at
+  // positions prefixes[s] + i of request batch_requests[s]. Unless
+  // scheduler_owned, the rows are validated on the device and the host waits
+  // for the per-row codes; scheduler-owned inputs are only normalised, with
+  // no host wait.
+  PagedMetadata(const at::Tensor& locations, const at::Tensor& batch_requests, const at::Tensor& positions,
+                const at::Tensor& mapping, const std::vector<int64_t>& prefixes, const std::vector<int64_t>& lengths,
+                int64_t slots, const at::Tensor& token_ids, int64_t vocabulary, bool scheduler_owned,
+                bool fuse_scheduler_plan) {
+    TORCH_CHECK(!fuse_scheduler_plan || scheduler_owned,
+                "GaudiRT device metadata: fused plan requires scheduler-owned inputs");
+    const int device = current_device();
+    const auto on_device = [device](const at::Tensor& t) { return t.is_cuda() && t.device().index() == device; };
+    const auto index_type = [](const at::Tensor& t) {
+      return t.scalar_type() == at::kInt || t.scalar_type() == at::kLong;
     };
-    locations_ = upload(locations_h_, {m});
-    requests_ = upload(requests_h_, {m});
-    positions_ = upload(positions_h_, {m});
-    mapping_ = upload(mapping_h_, {request_count, context});
-    const std::vector<int32_t> header{static_cast<int32_t>(m)};
-    header_ = upload(header, {1});
+    for (const auto& tensor : {locations, batch_requests})
+      TORCH_CHECK(on_device(tensor) && tensor.dim() == 1 && index_type(tensor),
+                  "GaudiRT device metadata: expected gaudirt int32 or int64 vectors");
+    const bool positions_on_cpu = fuse_scheduler_plan && positions.device().is_cpu();
+    TORCH_CHECK(positions.dim() == 1 &&
+                    ((positions_on_cpu && positions.scalar_type() == at::kLong && positions.is_contiguous()) ||
+                     (on_device(positions) && index_type(positions))),
+                "GaudiRT device metadata: invalid position input");
+    TORCH_CHECK(on_device(mapping) && mapping.scalar_type() == at::kInt && mapping.dim() == 2 && mapping.is_contiguous(),
+                "GaudiRT device metadata: expected a contiguous gaudirt int32 request map");
+    const int64_t m = locations.numel(), batch = batch_requests.numel();
+    const int64_t request_count = mapping.size(0), context = mapping.size(1);
+    const bool has_tokens = token_ids.defined();
+    TORCH_CHECK((has_tokens && on_device(token_ids) && token_ids.dim() == 1 && token_ids.numel() == m &&
+                 index_type(token_ids) && vocabulary > 0 && vocabulary <= std::numeric_limits<int32_t>::max()) ||
+                    (!has_tokens && vocabulary == 0),
+                "GaudiRT device metadata: invalid token ID inputs or vocabulary");
+    TORCH_CHECK(m > 0 && m <= kMaxRows && positions.numel() == m && batch > 0 && batch <= m &&
+                    static_cast<int64_t>(prefixes.size()) == batch && static_cast<int64_t>(lengths.size()) == batch &&
+                    slots > 0 && slots <= std::numeric_limits<int32_t>::max() && request_count > 0 &&
+                    request_count <= std::numeric_limits<int32_t>::max() && context > 0 &&
+                    context <= std::numeric_limits<int32_t>::max() &&
+                    mapping.numel() <= std::numeric_limits<int32_t>::max(),
+                "GaudiRT device metadata: dimensions outside supported range");
+    const int64_t bucket = static_cast<int64_t>(std::bit_ceil(static_cast<uint64_t>(m)));
+    std::vector<int32_t> row_seq(m), seq_prefix(batch), seq_first(batch), last(batch);
+    std::vector<int64_t> seq_visible(batch);
+    positions_h_.resize(m);
+    int64_t cursor = 0, visible = 0;
+    for (int64_t s = 0; s < batch; ++s) {
+      const int64_t prefix = prefixes[s], length = lengths[s];
+      TORCH_CHECK(prefix >= 0 && prefix < context && length > 0 && length <= context - prefix && length <= m - cursor,
+                  "GaudiRT device metadata: invalid sequence lengths");
+      sequences_.push_back({static_cast<int32_t>(cursor), static_cast<int32_t>(length), static_cast<int32_t>(prefix)});
+      seq_prefix[s] = static_cast<int32_t>(prefix);
+      seq_first[s] = static_cast<int32_t>(cursor);
+      seq_visible[s] = visible;
+      visible += prefix + length;
+      for (int64_t i = 0; i < length; ++i, ++cursor) {
+        row_seq[cursor] = static_cast<int32_t>(s);
+        positions_h_[cursor] = static_cast<int32_t>(prefix + i);
+      }
+      last[s] = static_cast<int32_t>(cursor - 1);
+    }
+    TORCH_CHECK(cursor == m, "GaudiRT device metadata: sequence lengths do not cover token rows");
+    if (positions_on_cpu) {
+      const auto* host_positions = positions.data_ptr<int64_t>();
+      for (int64_t row = 0; row < m; ++row)
+        TORCH_CHECK(host_positions[row] == positions_h_[row],
+                    "GaudiRT device metadata: host position does not match scheduler lengths");
+    }
+    // One buffer: host-staged words first (one copy), then the device outputs.
+    int64_t words = 0;
+    const auto header_offset = reserve_words(words, 1);
+    const auto last_offset = reserve_words(words, batch);
+    const auto row_seq_offset = reserve_words(words, m);
+    const auto prefix_offset = reserve_words(words, batch);
+    const auto first_offset = reserve_words(words, batch);
+    const auto visible_offset = reserve_words(words, 2 * batch);
+    const auto model_offset = positions_on_cpu ? reserve_words(words, 2 * m) : 0;
+    const auto staged_words = words;
+    const auto locations_offset = reserve_words(words, bucket);
+    const auto requests_offset = reserve_words(words, bucket);
+    const auto positions_offset = reserve_words(words, bucket);
+    const auto tokens_offset = has_tokens ? reserve_words(words, bucket) : 0;
+    // Codes, token codes and page flags are adjacent: one read-back.
+    const auto status_offset = scheduler_owned ? 0 : reserve_words(words, 2 * bucket + 1);
+    std::vector<int32_t> host(staged_words, 0);
+    host[header_offset] = static_cast<int32_t>(m);
+    std::copy(last.begin(), last.end(), host.begin() + last_offset);
+    std::copy(row_seq.begin(), row_seq.end(), host.begin() + row_seq_offset);
+    std::copy(seq_prefix.begin(), seq_prefix.end(), host.begin() + prefix_offset);
+    std::copy(seq_first.begin(), seq_first.end(), host.begin() + first_offset);
+    std::memcpy(host.data() + visible_offset, seq_visible.data(), batch * sizeof(int64_t));
+    if (positions_on_cpu) std::memcpy(host.data() + model_offset, positions.data_ptr<int64_t>(), m * sizeof(int64_t));
+    storage_ = upload_words(host, words);
+    int32_t* base = storage_.data_ptr<int32_t>();
+    header_ = storage_.narrow(0, header_offset, 1);
+    last_token_indices_ = storage_.narrow(0, last_offset, batch);
+    locations_ = storage_.narrow(0, locations_offset, m);
+    requests_ = storage_.narrow(0, requests_offset, m);
+    positions_ = storage_.narrow(0, positions_offset, m);
+    if (has_tokens) token_ids_ = storage_.narrow(0, tokens_offset, m);
+    if (positions_on_cpu)
+      model_positions_ = storage_.narrow(0, model_offset, 2 * m).view(at::kLong);
+    else if (fuse_scheduler_plan)
+      model_positions_ = positions;
+    mapping_ = mapping;
+    rows_ = m;
+    slots_ = slots;
+    request_count_ = request_count;
+    context_ = context;
+    vocabulary_ = vocabulary;
+
+    // Strided inputs are packed first (the kernels read dense vectors).
+    const auto dense = [](const at::Tensor& t) { return t.is_contiguous() ? t : t.contiguous(); };
+    const auto loc = dense(locations), req = dense(batch_requests);
+    const auto pos = positions_on_cpu ? model_positions_ : dense(positions);
+    const auto tok = has_tokens ? dense(token_ids) : at::Tensor();
+    gk_metadata_params p{};
+    p.struct_size = sizeof(p);
+    p.locations = loc.data_ptr();
+    p.locations_int64 = loc.scalar_type() == at::kLong;
+    p.batch_requests = req.data_ptr();
+    p.requests_int64 = req.scalar_type() == at::kLong;
+    p.positions = pos.data_ptr();
+    p.positions_int64 = pos.scalar_type() == at::kLong;
+    p.token_ids = has_tokens ? tok.data_ptr() : nullptr;
+    p.tokens_int64 = has_tokens && tok.scalar_type() == at::kLong;
+    p.row_seq = base + row_seq_offset;
+    p.seq_prefix = base + prefix_offset;
+    p.seq_first_row = base + first_offset;
+    p.seq_visible = reinterpret_cast<const int64_t*>(base + visible_offset);
+    p.visible_total = visible;
+    p.rows = static_cast<int32_t>(m);
+    p.padded_rows = static_cast<int32_t>(bucket);
+    p.batch = static_cast<int32_t>(batch);
+    p.requests = static_cast<int32_t>(request_count);
+    p.context = static_cast<int32_t>(context);
+    p.vocabulary = static_cast<int32_t>(vocabulary);
+    p.slots = slots;
+    p.out_locations = base + locations_offset;
+    p.out_requests = base + requests_offset;
+    p.out_positions = base + positions_offset;
+    p.out_tokens = has_tokens ? base + tokens_offset : nullptr;
+    at::Tensor workspace;
+    if (!scheduler_owned) {
+      p.mapping = mapping.data_ptr<int32_t>();
+      p.status = base + status_offset;
+      p.token_status = base + status_offset + bucket;
+      p.page_flags = base + status_offset + 2 * bucket;
+      const size_t need = gk_metadata_workspace_bytes(p.rows, p.batch);
+      workspace = at::empty({static_cast<int64_t>(need)}, mapping.options().dtype(at::kByte));
+      check_gk(gk_metadata_normalize(&p, workspace.data_ptr(), need, current_stream()), "GaudiRT device metadata");
+      // The reference's checked constructor also waits here for the codes.
+      const auto flags = storage_.narrow(0, status_offset, 2 * bucket + 1).cpu();
+      const int32_t* codes = flags.data_ptr<int32_t>();
+      for (int64_t row = 0; row < m; ++row)
+        TORCH_CHECK(codes[row] == 0, "GaudiRT device metadata: invalid scheduler metadata at row ", row, ", code ",
+                    codes[row]);
+      if (has_tokens)
+        for (int64_t row = 0; row < m; ++row)
+          TORCH_CHECK(codes[bucket + row] == 0, "GaudiRT device metadata: token ID outside vocabulary at row ", row);
+      page_ = 1;
+      for (int k = 9; k >= 0; --k)
+        if (!(codes[2 * bucket] & (1 << k))) {
+          page_ = int64_t{2} << k;
+          break;
+        }
+    } else {
+      check_gk(gk_metadata_normalize(&p, nullptr, 0, current_stream()), "GaudiRT device metadata");
+      page_ = 1;  // no host wait: the plan reads the token-granular map
+    }
+  }
+
+  static c10::intrusive_ptr<PagedMetadata> from_device(const at::Tensor& locations, const at::Tensor& batch_requests,
+                                                       const at::Tensor& positions, const at::Tensor& mapping,
+                                                       std::vector<int64_t> prefixes, std::vector<int64_t> lengths,
+                                                       int64_t slots) {
+    return c10::make_intrusive<PagedMetadata>(locations, batch_requests, positions, mapping, prefixes, lengths, slots,
+                                              at::Tensor(), 0, false, false);
+  }
+  static c10::intrusive_ptr<PagedMetadata> from_device_with_tokens(
+      const at::Tensor& locations, const at::Tensor& batch_requests, const at::Tensor& positions,
+      const at::Tensor& mapping, std::vector<int64_t> prefixes, std::vector<int64_t> lengths, int64_t slots,
+      const at::Tensor& token_ids, int64_t vocabulary) {
+    return c10::make_intrusive<PagedMetadata>(locations, batch_requests, positions, mapping, prefixes, lengths, slots,
+                                              token_ids, vocabulary, false, false);
+  }
+  // Scheduler inputs were checked at request entry; slots and request maps
+  // come from the scheduler's own pools.
+  static c10::intrusive_ptr<PagedMetadata> from_scheduler(const at::Tensor& locations, const at::Tensor& batch_requests,
+                                                          const at::Tensor& positions, const at::Tensor& mapping,
+                                                          std::vector<int64_t> prefixes, std::vector<int64_t> lengths,
+                                                          int64_t slots, const c10::optional<at::Tensor>& token_ids,
+                                                          int64_t vocabulary) {
+    return c10::make_intrusive<PagedMetadata>(locations, batch_requests, positions, mapping, prefixes, lengths, slots,
+                                              token_ids.value_or(at::Tensor()), vocabulary, true, false);
+  }
+  static c10::intrusive_ptr<PagedMetadata> from_scheduler_fused(
+      const at::Tensor& locations, const at::Tensor& batch_requests, const at::Tensor& positions,
+      const at::Tensor& mapping, std::vector<int64_t> prefixes, std::vector<int64_t> lengths, int64_t slots,
+      const c10::optional<at::Tensor>& token_ids, int64_t vocabulary, int64_t query_heads, int64_t kv_heads,
+      int64_t head_dim) {
+    auto metadata = c10::make_intrusive<PagedMetadata>(locations, batch_requests, positions, mapping, prefixes, lengths,
+                                                       slots, token_ids.value_or(at::Tensor()), vocabulary, true, true);
+    metadata->attention_plan(query_heads, kv_heads, head_dim);
+    return metadata;
   }
 
   int64_t rows() const { return rows_; }
@@ -279,18 +517,18 @@ class PagedMetadata : public torch::CustomClassHolder {
   at::Tensor row_requests() const { return requests_; }
   at::Tensor request_mapping() const { return mapping_; }
   at::Tensor model_positions() const {
-    TORCH_CHECK(false, "GaudiRT: model positions require fused scheduler metadata");
-    return {};
+    TORCH_CHECK(model_positions_.defined(), "GaudiRT: model positions require fused scheduler metadata");
+    return model_positions_;
   }
   at::Tensor last_token_indices() const {
-    TORCH_CHECK(false, "GaudiRT: last-token indices require batched metadata");
-    return {};
+    TORCH_CHECK(last_token_indices_.defined(), "GaudiRT: last-token indices require batched metadata");
+    return last_token_indices_;
   }
   at::Tensor token_ids() const {
-    TORCH_CHECK(false, "GaudiRT: token IDs were not validated in this metadata");
-    return {};
+    TORCH_CHECK(token_ids_.defined(), "GaudiRT: token IDs were not validated in this metadata");
+    return token_ids_;
   }
-  int64_t vocabulary() const { return 0; }
+  int64_t vocabulary() const { return vocabulary_; }
   std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, int64_t>
   forward_tensors(int64_t query_heads, int64_t kv_heads, int64_t head_dim) {
     return {token_ids(), last_token_indices(), rotary_positions(), rotary_header(), row_locations(),
@@ -330,20 +568,18 @@ class PagedMetadata : public torch::CustomClassHolder {
     // Block tables: the largest power-of-two page P (<= 1024) for which every
     // visible token t of every request sits at mapping[r, t - t % P] + t % P
     // with a P-aligned page start; P = 1 keeps the token-granular map.
-    const int64_t page = page_size();
+    const bool host_map = !mapping_h_.empty();
+    const int64_t page = host_map ? page_size() : page_;
     const int64_t max_pages = std::max<int64_t>(1, (context_ + page - 1) / page);
-    std::vector<int32_t> tables(request_count_ * max_pages, -1);
-    for (int64_t r = 0; r < request_count_; ++r)
-      for (int64_t t = 0; t <= max_position_[r]; t += page)
-        tables[r * max_pages + t / page] = mapping_h_[r * context_ + t] / static_cast<int32_t>(page);
     // Split the rows: runs of >= kPrefillMinRows consecutive positions become
     // prefill sequences (MFMA tiles of rows x heads) when the prefill kernel
-    // supports the geometry; every other row is a decode row.
+    // supports the geometry; every other row is a decode row. The requests of
+    // device-built metadata are filled in on the device below.
     const bool prefill_ok = (head_dim == 64 || head_dim == 128) && page >= 32 && query_heads / kv_heads <= 128;
     std::vector<int32_t> dec_request, dec_context, dec_map, seq_request, seq_first, seq_rows, seq_prefix;
     for (const auto& run : sequences_) {
       if (prefill_ok && run.length >= kPrefillMinRows) {
-        seq_request.push_back(requests_h_[run.row]);
+        seq_request.push_back(host_map ? requests_h_[run.row] : 0);
         seq_first.push_back(run.row);
         seq_rows.push_back(run.length);
         seq_prefix.push_back(run.prefix);
@@ -351,7 +587,7 @@ class PagedMetadata : public torch::CustomClassHolder {
         continue;
       }
       for (int32_t i = run.row; i < run.row + run.length; ++i) {
-        dec_request.push_back(requests_h_[i]);
+        dec_request.push_back(host_map ? requests_h_[i] : 0);
         dec_context.push_back(positions_h_[i] + 1);
         dec_map.push_back(i);
         info->decode_max_context = std::max<int64_t>(info->decode_max_context, positions_h_[i] + 1);
@@ -373,11 +609,37 @@ class PagedMetadata : public torch::CustomClassHolder {
     info->seq_first_row_offset = append(seq_first);
     info->seq_rows_offset = append(seq_rows);
     info->seq_prefix_offset = append(seq_prefix);
+    std::vector<int32_t> tables;
+    if (host_map) {
+      tables.assign(request_count_ * max_pages, -1);
+      for (int64_t r = 0; r < request_count_; ++r)
+        for (int64_t t = 0; t <= max_position_[r]; t += page)
+          tables[r * max_pages + t / page] = mapping_h_[r * context_ + t] / static_cast<int32_t>(page);
+    }
     info->block_table_offset = append(tables);
+    while (words.size() % 4) words.push_back(0);
+    const int64_t total = host_map ? static_cast<int64_t>(words.size()) : info->block_table_offset + request_count_ * max_pages;
     info->block_size = page;
     info->bt_stride = max_pages;
-    auto host = at::from_blob(words.data(), {static_cast<int64_t>(words.size())}, at::TensorOptions().dtype(at::kInt));
-    info->storage = host.to(device_int32().device(), false, true);
+    info->storage = upload_words(words, total);
+    if (!host_map) {
+      auto& storage = info->storage;
+      const auto section = [&](int64_t offset, int64_t count) { return storage.narrow(0, offset, count); };
+      if (info->decode_rows)
+        section(info->row_request_offset, info->decode_rows)
+            .copy_(requests_.index_select(0, section(info->row_map_offset, info->decode_rows)));
+      if (info->prefill_seqs)
+        section(info->seq_request_offset, info->prefill_seqs)
+            .copy_(requests_.index_select(0, section(info->seq_first_row_offset, info->prefill_seqs)));
+      if (page == 1)
+        section(info->block_table_offset, request_count_ * context_).copy_(mapping_.reshape({-1}));
+      else
+        check_gk(gk_block_tables(mapping_.data_ptr<int32_t>(), static_cast<int32_t>(request_count_),
+                                 static_cast<int32_t>(context_), static_cast<int32_t>(page),
+                                 storage.data_ptr<int32_t>() + info->block_table_offset,
+                                 static_cast<int32_t>(max_pages), info->stream),
+                 "GaudiRT attention: block tables");
+    }
     auto plan = make_plan_tensor(std::move(info));
     plans_.emplace(window, plan);
     return plan;
@@ -403,10 +665,12 @@ class PagedMetadata : public torch::CustomClassHolder {
     return 1;
   }
 
-  int64_t rows_ = 0, slots_ = 0, request_count_ = 0, context_ = 0;
+  int64_t rows_ = 0, slots_ = 0, request_count_ = 0, context_ = 0, vocabulary_ = 0, page_ = 1;
+  // Host copies (host constructor only; device metadata keeps positions_h_).
   std::vector<int32_t> locations_h_, requests_h_, positions_h_, mapping_h_, max_position_;
   std::vector<Sequence> sequences_;
-  at::Tensor locations_, requests_, positions_, mapping_, header_;
+  at::Tensor storage_, locations_, requests_, positions_, mapping_, header_, token_ids_, last_token_indices_,
+      model_positions_;
   std::unordered_map<int64_t, at::Tensor> plans_;
 };
 
@@ -578,6 +842,78 @@ std::tuple<at::Tensor, at::Tensor> advance_decode_lengths(const at::Tensor& seq_
   return {next, orig_next};
 }
 
+// ---------------------------------------------------------------------------
+// Paged slot allocator (src/bridge/paged_slot_allocator.cpp:91-190).
+// ---------------------------------------------------------------------------
+void require_indices(const at::Tensor& tensor) {
+  TORCH_CHECK(tensor.is_cuda() && tensor.device().index() == current_device() && tensor.scalar_type() == at::kLong &&
+                  tensor.dim() == 1 && tensor.is_contiguous(),
+              "GaudiRT paged allocator: expected contiguous device int64 indices");
+}
+
+// New slots for the next lengths[s] tokens of each sequence: the tail of the
+// page holding last_slots[s] first, then whole pages from free_pages in order.
+// Returns (slots [sum(lengths)] int64, pages taken from free_pages).
+std::tuple<at::Tensor, int64_t> allocate_paged_slots(const at::Tensor& last_slots, const at::Tensor& free_pages,
+                                                     const std::vector<int64_t>& prefixes,
+                                                     const std::vector<int64_t>& lengths, int64_t page_size) {
+  require_indices(last_slots);
+  require_indices(free_pages);
+  TORCH_CHECK(page_size >= 1 && page_size <= std::numeric_limits<int32_t>::max() && !prefixes.empty() &&
+                  prefixes.size() <= (size_t{1} << 30) && prefixes.size() == lengths.size() &&
+                  last_slots.numel() == static_cast<int64_t>(prefixes.size()),
+              "GaudiRT paged allocator: unsupported page size or request count");
+  const int64_t batch = static_cast<int64_t>(prefixes.size());
+  std::vector<int64_t> meta(4 * batch);
+  int64_t total = 0, pages = 0;
+  for (int64_t s = 0; s < batch; ++s) {
+    const int64_t prefix = prefixes[s], length = lengths[s];
+    TORCH_CHECK(prefix >= 0 && length >= 0 && prefix + length <= std::numeric_limits<int32_t>::max(),
+                "GaudiRT paged allocator: invalid request lengths");
+    meta[4 * s] = prefix;
+    meta[4 * s + 1] = length;
+    meta[4 * s + 2] = total;
+    meta[4 * s + 3] = pages;
+    total += length;
+    pages += (prefix + length + page_size - 1) / page_size - (prefix + page_size - 1) / page_size;
+  }
+  TORCH_CHECK(total > 0 && total <= (int64_t{1} << 30) && pages <= (int64_t{1} << 30) && pages <= free_pages.numel(),
+              "GaudiRT paged allocator: invalid token count or insufficient free pages");
+  if (page_size == 1) return {free_pages.narrow(0, 0, total).clone(), total};
+  std::vector<int32_t> words(meta.size() * 2);
+  std::memcpy(words.data(), meta.data(), meta.size() * sizeof(int64_t));
+  const auto device_meta = upload_words(words, static_cast<int64_t>(words.size()));
+  auto slots = at::empty({total}, last_slots.options());
+  check_gk(gk_paged_alloc_slots(last_slots.data_ptr<int64_t>(), free_pages.data_ptr<int64_t>(),
+                                reinterpret_cast<const int64_t*>(device_meta.data_ptr<int32_t>()),
+                                static_cast<int32_t>(batch), page_size, total, slots.data_ptr<int64_t>(),
+                                current_stream()),
+           "GaudiRT paged allocator");
+  return {slots, pages};
+}
+
+// Distinct pages of the released slots in order of first occurrence. Waits
+// for the count, as the reference does.
+at::Tensor release_paged_slots(const at::Tensor& slots, int64_t page_size, int64_t max_pages) {
+  require_indices(slots);
+  TORCH_CHECK(page_size >= 1 && page_size <= std::numeric_limits<int32_t>::max() && max_pages > 0 &&
+                  max_pages <= std::numeric_limits<int32_t>::max() && slots.numel() > 0 &&
+                  slots.numel() <= (int64_t{1} << 30),
+              "GaudiRT paged allocator: invalid release geometry");
+  const size_t need = gk_paged_release_workspace_bytes(max_pages);
+  auto workspace = at::empty({static_cast<int64_t>(need)}, slots.options().dtype(at::kByte));
+  auto pages = at::empty_like(slots);
+  auto count = at::empty({1}, slots.options().dtype(at::kInt));
+  check_gk(gk_paged_release_slots(slots.data_ptr<int64_t>(), slots.numel(), page_size, max_pages,
+                                  workspace.data_ptr(), need, pages.data_ptr<int64_t>(), count.data_ptr<int32_t>(),
+                                  current_stream()),
+           "GaudiRT paged allocator");
+  const int32_t released = count.cpu().data_ptr<int32_t>()[0];
+  TORCH_CHECK(released > 0 && released <= slots.numel(),
+              "GaudiRT paged allocator: released slot is outside the KV pool");
+  return pages.narrow(0, 0, released);
+}
+
 }  // namespace
 }  // namespace gaudirt_amd
 
@@ -585,6 +921,10 @@ TORCH_LIBRARY(gaudirt, m) {
   using gaudirt_amd::PagedMetadata;
   m.class_<PagedMetadata>("PagedMetadata")
       .def(torch::init<at::Tensor, at::Tensor, at::Tensor, at::Tensor, int64_t>())
+      .def_static("from_device", &PagedMetadata::from_device)
+      .def_static("from_device_with_tokens", &PagedMetadata::from_device_with_tokens)
+      .def_static("_from_scheduler", &PagedMetadata::from_scheduler)
+      .def_static("_from_scheduler_fused", &PagedMetadata::from_scheduler_fused)
       .def("rows", &PagedMetadata::rows)
       .def("slots", &PagedMetadata::slots)
       .def("context", &PagedMetadata::context)
@@ -617,6 +957,8 @@ TORCH_LIBRARY_IMPL(gaudirt, CUDA, m) {
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_allocate_paged_kv", &gaudirt_amd::allocate_paged_kv, "zeroed head-major bf16 KV pool");
+  m.def("_allocate_paged_slots", &gaudirt_amd::allocate_paged_slots, "page-granular KV slots for new tokens");
+  m.def("_release_paged_slots", &gaudirt_amd::release_paged_slots, "distinct pages of released KV slots");
   m.def("_kv_allocator_stats", &gaudirt_amd::allocator_stats, pybind11::arg("device") = 0);
   m.def("_paged_attn_kv_tile", [](int64_t) { return 512; });
   m.def("version", []() { return std::string(gk_version()); });

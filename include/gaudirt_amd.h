@@ -177,6 +177,93 @@ int gk_advance_decode_lengths(const int64_t* seq_lens, const int32_t* orig_seq_l
                               int64_t* next, int32_t* orig_next, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Device metadata: normalisation and validation of device-resident scheduler
+ * inputs. Replaces the gk_paged_metadata_i32_v1 / gk_scheduler_metadata_i32_v1
+ * and gk_token_indices_i32_v1 / gk_scheduler_tokens_i32_v1 launches of
+ * PagedMetadata's device constructor (src/bridge/paged_metadata.cpp:26-80,
+ * 176-430).
+ *
+ * Sequence s owns rows [seq_first_row[s], seq_first_row[s+1]) at positions
+ * seq_prefix[s] + i of block-table row batch_requests[s]; row_seq[r] is the
+ * sequence of row r. Outputs are int32 [padded_rows] (zero past rows).
+ *
+ * With mapping and status both set, status[r] receives one code per row
+ * (0 = valid), as the reference's device validation reports them:
+ *   1 location outside [0, slots) or position outside [0, context) (int64
+ *     values that do not fit included)
+ *   2 batch_requests[s] outside [0, requests)
+ *   3 mapping[request, position] != location
+ *   4 the row's location is the output slot of an earlier row
+ *   5 position != seq_prefix[s] + (r - seq_first_row[s])
+ *   6 (first row of s) some prefix position t < prefix + length of the
+ *     sequence's request has no slot (mapping < 0)
+ *   7 (first row of s) a prefix slot is the output slot of another
+ *     (request, position)
+ * A row keeps the first code in the order 1, 2, 3, 5, 4, 6, 7. With
+ * page_flags set, bit k of *page_flags is cleared iff every visible token t
+ * of every sequence sits at mapping[t & ~(P-1)] + (t & (P-1)) with that page
+ * start P-aligned, for P = 2 << k (k < 10). With mapping NULL nothing is
+ * checked (scheduler-owned inputs) and no workspace is needed.
+ * seq_visible[s] = sum over earlier sequences of (prefix + length);
+ * visible_total = the sum over all.
+ * ------------------------------------------------------------------------- */
+typedef struct gk_metadata_params {
+  size_t struct_size;           /* sizeof(gk_metadata_params) as the caller was built; checked */
+  const void* locations;        /* [rows] int32 or int64 (locations_int64) */
+  const void* batch_requests;   /* [batch] */
+  const void* positions;        /* [rows] */
+  const void* token_ids;        /* [rows] or NULL */
+  int32_t locations_int64, requests_int64, positions_int64, tokens_int64;
+  const int32_t* mapping;       /* [requests, context] or NULL */
+  const int32_t* row_seq;       /* [rows] */
+  const int32_t* seq_prefix;    /* [batch] */
+  const int32_t* seq_first_row; /* [batch] */
+  const int64_t* seq_visible;   /* [batch] */
+  int64_t visible_total;
+  int32_t rows, padded_rows, batch, requests, context, vocabulary;
+  int64_t slots;
+  int32_t* out_locations;       /* [padded_rows] */
+  int32_t* out_requests;        /* [padded_rows] request of each row */
+  int32_t* out_positions;       /* [padded_rows] */
+  int32_t* out_tokens;          /* [padded_rows] when token_ids is set */
+  int32_t* status;              /* [padded_rows] or NULL */
+  int32_t* token_status;        /* [padded_rows] 1 = token outside [0, vocabulary), or NULL */
+  int32_t* page_flags;          /* [1] or NULL */
+} gk_metadata_params;
+
+size_t gk_metadata_workspace_bytes(int32_t rows, int32_t batch);
+int gk_metadata_normalize(const gk_metadata_params* params, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream);
+
+/* Block tables of a request map whose visible tokens are page-aligned with
+ * page size P (a power of two <= 1024): tables[r * pages + k] =
+ * mapping[r, k P] / P (-1 where that slot is negative or k P >= context).
+ * Replaces the per-token gather indices of gk_attn_tile_indices_i32_v1
+ * (src/bridge/attention_plan.cpp:36-57) for page-aligned maps. */
+int gk_block_tables(const int32_t* mapping, int32_t requests, int32_t context, int32_t page_size,
+                    int32_t* tables, int32_t pages, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged slot allocator (gk_paged_alloc_i32_v1 / gk_paged_free_i32_v1 of
+ * src/bridge/paged_slot_allocator.cpp:91-190).
+ *
+ * Allocation: seq_meta[4 s .. 4 s + 3] = {prefix, length, first output index,
+ * first free page} (int64, device). Sequence s's first min(length,
+ * (-prefix) mod P) new tokens continue at last_slots[s] + 1, + 2, ...; the rest
+ * fill pages free_pages[first free page], ... in order, P tokens per page.
+ * out_slots [total] int64.
+ * ------------------------------------------------------------------------- */
+int gk_paged_alloc_slots(const int64_t* last_slots, const int64_t* free_pages, const int64_t* seq_meta,
+                         int32_t batch, int64_t page_size, int64_t total, int64_t* out_slots, hipStream_t stream);
+
+/* Release: the distinct pages slot / P of slots[0 .. n), in order of first
+ * occurrence, into out_pages; *out_count (device int32) = their number, or -1
+ * when a slot's page lies outside [1, max_pages] (page 0 is reserved). */
+size_t gk_paged_release_workspace_bytes(int64_t max_pages);
+int gk_paged_release_slots(const int64_t* slots, int64_t n, int64_t page_size, int64_t max_pages, void* workspace,
+                           size_t workspace_bytes, int64_t* out_pages, int32_t* out_count, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Stream-ordered block allocator (replaces runtime::BlockCachingAllocator,
  * include/gaudirt/runtime/block_caching_allocator.hpp:19-70, for this path).
  * HBM slabs from hipMalloc, carved into 256-byte aligned blocks by best fit.

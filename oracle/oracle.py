@@ -31,6 +31,22 @@ Parity status (how each oracle function is pinned; see tests/test_oracle.py):
 - ``check_tolerance`` / ``bf16_ulp``: known answers (one ulp allowed only where
   it exceeds 2e-2) and the seeded case where the fp64 answer itself is one ulp
   from direct_bf16_pv.
+- ``metadata_codes``: the rejection cases of
+  tests/paged_device_metadata_smoke.py:109-125 (codes 1, 2, 1, 3, 6, 7, 4 on the
+  reference test's own data), acceptance of every valid layout the smoke test
+  builds, and agreement of "all codes zero" with a set-based brute force of the
+  host constructor's accept/reject decision on random corruptions. Code 5
+  (position != prefix + offset) has no reference test vector: parity unpinned
+  beyond the brute force.
+- ``page_flags`` / ``largest_page``: closed forms (identity map -> 1024, a map
+  shifted by one slot -> 1, permuted pages of P -> P) and brute force over
+  random block tables.
+- ``allocate_paged_slots`` / ``release_paged_slots``: the expected values of
+  tests/paged_slots_device_smoke.py (evaluated literally for P = 16 and 64),
+  of tests/paged_attention_generalized_smoke.py:146-158 and
+  tests/dynamic_eager_ops_smoke.py:383-418, the rejected releases (page 0,
+  page max_pages + 1, 2^40), and invariants (slots distinct, slot % P ==
+  position % P, pages drawn in free-list order).
 """
 
 import ctypes
@@ -345,3 +361,132 @@ def check_tolerance(actual_bits, reference_bits, max_abs=2e-2, mean_abs=2e-3):
         f"> bound {bound.flat[worst]}")
     assert diff.mean() <= mean_abs, (float(diff.mean()), mean_abs)
     return float(diff.max()), float(diff.mean())
+
+
+# ---------------------------------------------------------------------------
+# Device metadata validation and the paged slot allocator (integer host logic,
+# small cases: pure Python).
+# ---------------------------------------------------------------------------
+
+def _ints(values):
+    return [int(v) for v in np.asarray(values).reshape(-1)]
+
+
+def metadata_codes(locations, batch_requests, positions, mapping, prefixes, lengths, slots):
+    """Per-row status codes of PagedMetadata's checked device constructor.
+
+    Follows the checks of the reference's host constructor
+    (src/bridge/paged_metadata.cpp:82-138) applied per row of the device layout
+    of :176-232 (sequence s owns the next lengths[s] rows at positions
+    prefixes[s] + i of request batch_requests[s]), with the codes the
+    reference's device validation reports (tests/paged_device_metadata_smoke.py:109-125):
+    1 location or position out of range, 2 request out of range, 3 mapping
+    disagrees, 5 position != prefix + offset, 4 an earlier row writes the same
+    slot, 6 / 7 (on a sequence's first row) a missing / aliased prefix slot.
+    A row keeps the first code in that order.
+    """
+    locations, positions = _ints(locations), _ints(positions)
+    batch_requests, prefixes, lengths = _ints(batch_requests), _ints(prefixes), _ints(lengths)
+    mapping = np.asarray(mapping)
+    request_count, context = mapping.shape
+    row_seq, first = [], []
+    for s, length in enumerate(lengths):
+        first.append(len(row_seq))
+        row_seq += [s] * length
+    rows = len(locations)
+    assert len(row_seq) == rows == len(positions)
+    codes = [0] * rows
+    owner = {}
+    for i in range(rows):
+        s = row_seq[i]
+        loc, pos, req = locations[i], positions[i], batch_requests[s]
+        if not (0 <= loc < slots and 0 <= pos < context):
+            codes[i] = 1
+        elif not 0 <= req < request_count:
+            codes[i] = 2
+        elif int(mapping[req, pos]) != loc:
+            codes[i] = 3
+        elif pos != prefixes[s] + i - first[s]:
+            codes[i] = 5
+        else:
+            owner.setdefault(loc, i)
+    for i in range(rows):
+        if codes[i] == 0 and owner[locations[i]] != i:
+            codes[i] = 4
+    for s, req in enumerate(batch_requests):
+        if not 0 <= req < request_count:
+            continue
+        missing = aliased = False
+        for t in range(prefixes[s] + lengths[s]):
+            slot = int(mapping[req, t])
+            if slot < 0:
+                missing = True
+                continue
+            o = owner.get(slot)
+            if o is not None and (batch_requests[row_seq[o]], positions[o]) != (req, t):
+                aliased = True
+        i = first[s]
+        if codes[i] == 0 and (missing or aliased):
+            codes[i] = 6 if missing else 7
+    return codes
+
+
+def page_flags(mapping, batch_requests, prefixes, lengths):
+    """Bit k set iff some visible token t < prefix + length of some sequence is
+    not at mapping[r, t & ~(P-1)] + (t & (P-1)) with a P-aligned page start,
+    for P = 2 << k (k < 10). The largest P with a clear bit is the page size
+    the attention plan can use for block tables (P = 1 when every bit is set)."""
+    mapping = np.asarray(mapping)
+    flags = 0
+    for req, prefix, length in zip(_ints(batch_requests), _ints(prefixes), _ints(lengths)):
+        if not 0 <= req < mapping.shape[0]:
+            continue
+        row = [int(v) for v in mapping[req]]
+        for k in range(10):
+            page = 2 << k
+            for t in range(prefix + length):
+                start = row[t - t % page]
+                if row[t] < 0 or start < 0 or start % page or row[t] != start + t % page:
+                    flags |= 1 << k
+                    break
+    return flags
+
+
+def largest_page(flags):
+    for k in range(9, -1, -1):
+        if not flags & (1 << k):
+            return 2 << k
+    return 1
+
+
+def allocate_paged_slots(last_slots, free_pages, prefixes, lengths, page_size):
+    """New KV slots for the next lengths[s] tokens of each sequence
+    (src/bridge/paged_slot_allocator.cpp:91-140): the first
+    min(length, (-prefix) mod P) continue after last_slots[s] in the page the
+    sequence already holds, the rest fill whole pages taken from free_pages in
+    order. Returns (slots, pages used)."""
+    free_pages = _ints(free_pages)
+    out, used = [], 0
+    for last, prefix, length in zip(_ints(last_slots), _ints(prefixes), _ints(lengths)):
+        existing = min(length, (-prefix) % page_size)
+        out += [last + 1 + i for i in range(existing)]
+        for i in range(length - existing):
+            out.append(free_pages[used + i // page_size] * page_size + i % page_size)
+        used += -(-(length - existing) // page_size)
+    return out, used
+
+
+def release_paged_slots(slots, page_size, max_pages):
+    """Distinct pages slot // P of the released slots in order of first
+    occurrence (src/bridge/paged_slot_allocator.cpp:142-190). Pages 1 ..
+    max_pages belong to the pool (page 0 is reserved); any other page raises
+    ValueError, as the reference rejects it ("outside the KV pool")."""
+    pages, seen = [], set()
+    for slot in _ints(slots):
+        page = slot // page_size if slot >= 0 else -1
+        if not 1 <= page <= max_pages:
+            raise ValueError("released slot is outside the KV pool")
+        if page not in seen:
+            seen.add(page)
+            pages.append(page)
+    return pages

@@ -87,3 +87,28 @@ def test_struct_size_guard_rejects_mismatched_callers(lib):
     q.struct_size = 8
     assert lib.gk_paged_prefill(ctypes.byref(q), None) == capi.GK_ERR_INVALID_ARGUMENT
     assert "struct_size" in lib.gk_last_error().decode()
+
+
+def test_metadata_and_allocator_validation(lib):
+    p = capi.MetadataParams()
+    p.struct_size = 16
+    assert lib.gk_metadata_normalize(ctypes.byref(p), None, 0, None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "struct_size" in lib.gk_last_error().decode()
+    p = capi.MetadataParams()
+    p.rows, p.padded_rows, p.batch, p.requests, p.context, p.slots = 4, 4, 5, 2, 64, 128
+    assert lib.gk_metadata_normalize(ctypes.byref(p), None, 0, None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "dimensions" in lib.gk_last_error().decode()  # batch > rows
+    p.batch = 2
+    assert lib.gk_metadata_normalize(ctypes.byref(p), None, 0, None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "null pointer" in lib.gk_last_error().decode()
+    # Validation needs the duplicate-slot table: 2 x pow2(>= 2 rows, >= 64) + batch words.
+    assert lib.gk_metadata_workspace_bytes(4, 2) == (64 * 2 + 2) * 4
+    assert lib.gk_metadata_workspace_bytes(100, 3) == (256 * 2 + 3) * 4
+    assert lib.gk_block_tables(None, 2, 64, 48, None, 2, None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert lib.gk_paged_alloc_slots(None, None, None, 1, 0, 4, None, None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert lib.gk_paged_release_workspace_bytes(512) == 513 * 4
+    rc = lib.gk_paged_release_slots(None, 4, 16, 0, None, 0, None, None, None)
+    assert rc == capi.GK_ERR_INVALID_ARGUMENT and "release geometry" in lib.gk_last_error().decode()
+    rc = lib.gk_paged_release_slots(ctypes.c_void_p(16), 4, 16, 512, ctypes.c_void_p(16), 8, ctypes.c_void_p(16),
+                                    ctypes.c_void_p(16), None)
+    assert rc == capi.GK_ERR_WORKSPACE

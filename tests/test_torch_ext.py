@@ -124,3 +124,34 @@ def test_fake_kernels_on_meta_tensors():
 def test_kv_tile_and_version(ext):
     assert gaudirt_amd.paged_attn_kv_tile(1) == 512
     assert ext.version().startswith("gaudirt_amd")
+
+
+def test_device_constructors_have_the_reference_signatures():
+    # TorchScript compiles the calls against the registered schemas, with the
+    # argument lists the reference's tests use
+    # (tests/paged_device_metadata_smoke.py:59-61, tests/scheduler_metadata_async_smoke.py:30-31,
+    # tests/scheduler_metadata_fused_smoke.py:36-46).
+    @torch.jit.script
+    def construct(l: torch.Tensor, r: torch.Tensor, p: torch.Tensor, m: torch.Tensor, t: torch.Tensor):
+        a = torch.classes.gaudirt.PagedMetadata.from_device(l, r, p, m, [2], [1], 16)
+        b = torch.classes.gaudirt.PagedMetadata.from_device_with_tokens(l, r, p, m, [2], [1], 16, t, 32000)
+        c = torch.classes.gaudirt.PagedMetadata._from_scheduler(l, r, p, m, [2], [1], 16, None, 0)
+        d = torch.classes.gaudirt.PagedMetadata._from_scheduler_fused(l, r, p, m, [2], [1], 16, t, 32000, 4, 2, 128)
+        return a, b, c, d
+
+    assert construct is not None
+
+
+def test_device_constructors_reject_host_tensors():
+    # Host tensors (or a box without a GPU) are refused before any device work.
+    locations, requests, positions, mapping = _base()
+    with pytest.raises(RuntimeError, match="GaudiRT"):
+        torch.classes.gaudirt.PagedMetadata.from_device(locations, requests, positions, mapping, [2, 3], [1, 1], 16)
+
+
+def test_slot_allocator_rejects_host_tensors(ext):
+    last = torch.tensor([-1], dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="GaudiRT"):
+        ext._allocate_paged_slots(last, torch.arange(4), [0], [3], 16)
+    with pytest.raises(RuntimeError, match="GaudiRT"):
+        ext._release_paged_slots(last, 16, 512)
