@@ -287,6 +287,51 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   f32x4_t o[S::NO];
   float m_run = -INFINITY, l_run = 0.f;
 
+  // Finished segments are not stored right away. The pipeline's waits count
+  // every vector memory operation older than the newest tile (vmcnt), so a
+  // store issued among the tile loads holds up the next wait until it is
+  // acknowledged, which under full read load takes about a tile's time. Up to
+  // two segments wait in registers instead and go out when the workgroup's
+  // pipeline has drained (or when a third one needs the room). With D = 256
+  // the registers are not there: segments are stored at once.
+  constexpr int kMaxPend = D <= 128 ? 2 : 0;
+  struct Pending {
+    f32x4_t v[S::NO];   // output rows already divided by l (output) or the raw partial
+    float m, l;         // partial: running max / sum of head c16 (lanes q == 0)
+    float* dst;         // output row block (bf16) or partial block (fp32) of head 0
+    int hv;             // valid heads
+    int out;            // 1: bf16 output, 0: partial
+    float* span;        // unit_span entry to write (nullptr: none)
+    int span0, span1;
+  };
+  Pending pend0, pend1;
+  int npend = 0;
+  auto flush = [&](const Pending& e) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * q + r;
+      if (h >= e.hv) continue;
+      if (e.out) {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(e.dst) + (int64_t)h * D + c16;
+#pragma unroll
+        for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(e.v[c][r]);
+      } else {
+        float* dst = e.dst + (int64_t)h * D + c16;
+#pragma unroll
+        for (int c = 0; c < S::NO; ++c) dst[16 * c] = e.v[c][r];
+      }
+    }
+    if (!e.out && q == 0 && c16 < e.hv) {
+      float* ml = a.part_ml + (e.dst - a.part_o) / D * 2 + (int64_t)c16 * 2;
+      ml[0] = e.m;
+      ml[1] = e.l;
+    }
+    if (e.span && lane == 0) {
+      e.span[0] = __int_as_float(e.span0);
+      e.span[1] = __int_as_float(e.span1);
+    }
+  };
+
   auto finalize = [&](const TileDesc& t) {
     l_run += shfl_xor(l_run, 16);
     l_run += shfl_xor(l_run, 32);
@@ -298,39 +343,47 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     const int hv = min(16, a.group - hg * 16);
     const int head0 = kvh * a.group + hg * 16;
     const int64_t g0 = t.g - t.j;  // the unit's first tile
-    if (g0 >= g_begin && g0 + t.count <= g_end) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int h = 4 * q + r;
-        if (h >= hv) continue;
-        const float inv = lrow[r] > 0.f ? 1.f / lrow[r] : 0.f;
-        uint16_t* dst = a.out + (int64_t)t.qrow * a.out_stride + (int64_t)(head0 + h) * D + c16;
-#pragma unroll
-        for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(o[c][r] * inv);
-      }
-    } else {
-      const int slot = 2 * w + (g0 <= g_begin ? 0 : 1);
-      const int64_t pi = (int64_t)slot * a.heads_per_group;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int h = 4 * q + r;
-        if (h >= hv) continue;
-        float* dst = a.part_o + (pi + h) * D + c16;
-#pragma unroll
-        for (int c = 0; c < S::NO; ++c) dst[16 * c] = o[c][r];
-      }
-      if (q == 0 && c16 < hv) {
-        a.part_ml[(pi + c16) * 2] = m_run;
-        a.part_ml[(pi + c16) * 2 + 1] = l_run;
-      }
+    if (kMaxPend == 2 && npend == 2) {
+      flush(pend0);
+      pend0 = pend1;
+      npend = 1;
     }
-    if (t.j == t.count - 1 && lane == 0) {
+    Pending e;
+    e.hv = hv;
+    e.m = m_run;
+    e.l = l_run;
+    if (g0 >= g_begin && g0 + t.count <= g_end) {
+      e.out = 1;
+      e.dst = reinterpret_cast<float*>(a.out + (int64_t)t.qrow * a.out_stride + (int64_t)head0 * D);
+      float inv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) inv[r] = lrow[r] > 0.f ? 1.f / lrow[r] : 0.f;
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e.v[c][r] = o[c][r] * inv[r];
+    } else {
+      e.out = 0;
+      const int slot = 2 * w + (g0 <= g_begin ? 0 : 1);
+      e.dst = a.part_o + (int64_t)slot * a.heads_per_group * D;
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) e.v[c] = o[c];
+    }
+    e.span = nullptr;
+    e.span0 = e.span1 = 0;
+    if (t.j == t.count - 1) {
       // This workgroup holds the unit's last tile: record where its partials are.
       const int64_t wf = g0 / per;
-      const int first_slot = (int)(2 * wf + (g0 == wf * per ? 0 : 1));
-      float* span = sa.unit_span + ((int64_t)t.row * U + t.h) * 2;
-      span[0] = __int_as_float(first_slot);
-      span[1] = __int_as_float(w);
+      e.span = sa.unit_span + ((int64_t)t.row * U + t.h) * 2;
+      e.span0 = (int)(2 * wf + (g0 == wf * per ? 0 : 1));
+      e.span1 = w;
+    }
+    if constexpr (kMaxPend == 0) {
+      flush(e);
+    } else {
+      if (npend == 0) pend0 = e;
+      else pend1 = e;
+      ++npend;
     }
   };
 
@@ -509,6 +562,9 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     consume(d1, kt1, vt1, qp1);
     if (!more) break;
   }
+  // Every tile has been consumed: store the segments still held.
+  if (kMaxPend > 0 && npend >= 1) flush(pend0);
+  if (kMaxPend > 0 && npend == 2) flush(pend1);
 }
 
 // ---------------------------------------------------------------------------
