@@ -4,8 +4,11 @@ Python view of the path, mirroring the reference's ``gaudirt`` operator API
 for it (python/gaudirt/__init__.py, src/bridge/generic_private_use1.cpp:430-540):
 
 - ``torch.ops.gaudirt.paged_attn`` / ``_paged_attn_validated`` /
-  ``_advance_decode_lengths`` and ``torch.classes.gaudirt.PagedMetadata`` are
-  registered by the HIP extension ``gaudirt_amd._C``;
+  ``_advance_decode_lengths``, the rotary ops ``rotary_embedding`` /
+  ``rotary_embedding_positions`` / ``_rotary_embedding_validated``, and
+  ``torch.classes.gaudirt.PagedMetadata`` are registered by the HIP extension
+  ``gaudirt_amd._C``, together with ``rotary_paged_attn`` (rotary embedding
+  fused into the attention's KV store; no counterpart in the reference);
 - ``allocate_paged_kv(layers, slots, kv_heads, head_dim)`` returns a zeroed
   head-major bf16 pool ``[layers, 2, kv_heads, slots, head_dim]`` from the
   stream-ordered block allocator, and ``kv_pool_views(pool, layer)`` its
@@ -67,6 +70,34 @@ def _register_fakes(torch):
     @torch.library.register_fake("gaudirt::_advance_decode_lengths")
     def _fake_advance_decode_lengths(seq_lens, orig_seq_lens):
         return torch.empty_like(seq_lens), torch.empty_like(orig_seq_lens)
+
+    @torch.library.register_fake("gaudirt::rotary_embedding")
+    def _fake_rotary_embedding(query, key, cache, metadata, head_dim, rotary_dim, is_neox):
+        torch._check(key.shape[0] == query.shape[0])
+        return (torch.empty_like(query, memory_format=torch.contiguous_format),
+                torch.empty_like(key, memory_format=torch.contiguous_format))
+
+    @torch.library.register_fake("gaudirt::rotary_embedding_positions")
+    def _fake_rotary_embedding_positions(query, key, cache, positions, head_dim, rotary_dim, is_neox):
+        torch._check(key.shape[0] == query.shape[0])
+        torch._check(positions.shape[0] == query.shape[0])
+        return (torch.empty_like(query, memory_format=torch.contiguous_format),
+                torch.empty_like(key, memory_format=torch.contiguous_format))
+
+    @torch.library.register_fake("gaudirt::_rotary_embedding_validated")
+    def _fake_rotary_embedding_validated(query, key, cache, positions, header, context, head_dim, rotary_dim,
+                                         is_neox):
+        torch._check(key.shape[0] == query.shape[0])
+        torch._check(positions.shape[0] == query.shape[0])
+        return (torch.empty_like(query, memory_format=torch.contiguous_format),
+                torch.empty_like(key, memory_format=torch.contiguous_format))
+
+    @torch.library.register_fake("gaudirt::rotary_paged_attn")
+    def _fake_rotary_paged_attn(query, key, value, key_pool, value_pool, cache, metadata, head_dim, rotary_dim,
+                                is_neox, scale, softcap=0.0, sliding_window=-1):
+        torch._check(key.shape[0] == query.shape[0])
+        torch._check(value.shape[0] == query.shape[0])
+        return torch.empty_like(query, memory_format=torch.contiguous_format)
 
 
 def allocate_paged_kv(layers, slots, kv_heads, head_dim):

@@ -29,7 +29,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", str(ROOT
           "-Wall", "-Wno-unused-function"]
 
 LIB_SOURCES = ["gk_api.cpp", "block_allocator.cpp", "kv_store.hip", "paged_decode.hip", "decode_stream.hip",
-               "paged_prefill.hip", "metadata.hip"]
+               "paged_prefill.hip", "metadata.hip", "rotary.hip"]
 LIB_NAME = "libgaudirt_amd.so"
 
 

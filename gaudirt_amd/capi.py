@@ -30,6 +30,7 @@ EXPORTED = [
     "gk_paged_alloc_slots", "gk_paged_release_workspace_bytes", "gk_paged_release_slots",
     "gk_allocator_create", "gk_allocator_destroy", "gk_allocator_alloc", "gk_allocator_record_stream",
     "gk_allocator_free", "gk_allocator_empty_cache", "gk_allocator_get_stats",
+    "gk_rotary_embedding", "gk_rotary_kv_store",
 ]
 
 c_void_p = ctypes.c_void_p
@@ -73,6 +74,21 @@ class PrefillParams(_Sized):
         ("q_heads", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32),
         ("scale", c_f32), ("softcap", c_f32), ("sliding_window", c_i32),
         ("out", c_void_p), ("out_row_stride", c_i64),
+    ]
+
+
+class RotaryParams(_Sized):
+    _fields_ = [
+        ("struct_size", ctypes.c_size_t),
+        ("query", c_void_p), ("q_row_stride", c_i64), ("q_width", c_i64),
+        ("key", c_void_p), ("k_row_stride", c_i64), ("k_width", c_i64),
+        ("positions", c_void_p), ("positions_int64", c_i32),
+        ("cos_sin", c_void_p), ("cache_rows", c_i64),
+        ("rows", c_i32), ("head_dim", c_i32), ("rotary_dim", c_i32), ("is_neox", c_i32),
+        ("q_out", c_void_p), ("q_out_row_stride", c_i64),
+        ("k_out", c_void_p), ("k_out_row_stride", c_i64),
+        ("value", c_void_p), ("v_row_stride", c_i64),
+        ("slot_mapping", c_void_p), ("pool", c_void_p), ("slots", c_i64), ("kv_heads", c_i32),
     ]
 
 
@@ -144,6 +160,8 @@ def load():
     lib.gk_allocator_free.argtypes = [c_void_p, c_void_p]
     lib.gk_allocator_empty_cache.argtypes = [c_void_p]
     lib.gk_allocator_get_stats.argtypes = [c_void_p, ctypes.POINTER(AllocatorStats)]
+    lib.gk_rotary_embedding.argtypes = [ctypes.POINTER(RotaryParams), c_void_p]
+    lib.gk_rotary_kv_store.argtypes = [ctypes.POINTER(RotaryParams), c_void_p]
     _lib = lib
     return lib
 

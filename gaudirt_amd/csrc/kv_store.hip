@@ -29,7 +29,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const uint16_t* __restric
     const int32_t kind = (int32_t)(rest & 1);
     const int32_t row = (int32_t)(rest >> 1);
     const int32_t slot = slot_mapping[row];
-    if (slot < 0) continue;
+    if (slot < 0 || slot >= slots) continue;  // negative: no store; past the pool: never written
     const uint16_t* src = (kind ? value + row * value_stride : key + row * key_stride) +
                           (int64_t)head * head_dim + chunk * 8;
     uint16_t* dst = pool + (((int64_t)kind * kv_heads + head) * slots + slot) * head_dim + chunk * 8;

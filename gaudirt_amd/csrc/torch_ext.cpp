@@ -695,14 +695,19 @@ at::Tensor kernel_rows(const at::Tensor& t) {
 // paged_attn_validated / paged_attn_internal (src/bridge/paged_attention.cpp:164-347):
 // store the rows' K/V into the pool, then attend every row over its request's
 // visible keys.
-at::Tensor paged_attn_validated(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
-                                const at::Tensor& key_pool, const at::Tensor& value_pool, const at::Tensor& locations,
-                                const at::Tensor& requests, const at::Tensor& positions, const at::Tensor& plan_tensor,
-                                const at::Tensor& header, int64_t head_dim, double scale, double softcap,
-                                int64_t sliding_window) {
-  (void)requests;
-  (void)positions;
-  (void)header;
+// Rotary embedding fused into the KV store of an attention call: the cos/sin
+// cache, the rows' positions and the rotation geometry.
+struct RotarySpec {
+  at::Tensor cache;      // bf16 [cache_rows, rotary_dim], contiguous
+  at::Tensor positions;  // int32 [rows], device
+  int64_t rotary_dim;
+  bool neox;
+};
+
+at::Tensor paged_attn_impl(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
+                           const at::Tensor& key_pool, const at::Tensor& value_pool, const at::Tensor& locations,
+                           const at::Tensor& plan_tensor, int64_t head_dim, double scale, double softcap,
+                           int64_t sliding_window, const RotarySpec* rotary) {
   const auto& plan = plan_data(plan_tensor);
   const hipStream_t stream = current_stream();
   const float scale_f = static_cast<float>(scale), softcap_f = static_cast<float>(softcap);
@@ -740,15 +745,47 @@ at::Tensor paged_attn_validated(const at::Tensor& query, const at::Tensor& key, 
               "GaudiRT attention: KV pool descriptor is not backed by combined storage");
   record_pool_stream(key_pool, stream);
 
-  const auto q = kernel_rows(query), k = kernel_rows(key), v = kernel_rows(value);
+  auto q = kernel_rows(query);
+  const auto k = kernel_rows(key), v = kernel_rows(value);
   auto output = bucket_output(query, plan.rows, query.size(1));
   void* pool = key_pool.data_ptr();
   // KV store first, on the same stream: rows of one sequence attend each
   // other's new keys.
-  check_gk(gk_kv_store(k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), locations.data_ptr<int32_t>(),
-                       static_cast<int32_t>(plan.rows), pool, plan.slots, static_cast<int32_t>(plan.kv_heads),
-                       static_cast<int32_t>(head_dim), stream),
-           "GaudiRT attention: KV store");
+  if (!rotary) {
+    check_gk(gk_kv_store(k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0), locations.data_ptr<int32_t>(),
+                         static_cast<int32_t>(plan.rows), pool, plan.slots, static_cast<int32_t>(plan.kv_heads),
+                         static_cast<int32_t>(head_dim), stream),
+             "GaudiRT attention: KV store");
+  } else {
+    // Rotated keys go straight into the pool; the rotated queries feed the attention.
+    auto q_rot = at::empty({plan.rows, query.size(1)}, query.options());
+    gk_rotary_params r{};
+    r.struct_size = sizeof(r);
+    r.query = q.data_ptr();
+    r.q_row_stride = q.stride(0);
+    r.q_width = q.size(1);
+    r.key = k.data_ptr();
+    r.k_row_stride = k.stride(0);
+    r.k_width = k.size(1);
+    r.positions = rotary->positions.data_ptr();
+    r.positions_int64 = 0;
+    r.cos_sin = rotary->cache.data_ptr();
+    r.cache_rows = rotary->cache.size(0);
+    r.rows = static_cast<int32_t>(plan.rows);
+    r.head_dim = static_cast<int32_t>(head_dim);
+    r.rotary_dim = static_cast<int32_t>(rotary->rotary_dim);
+    r.is_neox = rotary->neox ? 1 : 0;
+    r.q_out = q_rot.data_ptr();
+    r.q_out_row_stride = q_rot.stride(0);
+    r.value = v.data_ptr();
+    r.v_row_stride = v.stride(0);
+    r.slot_mapping = locations.data_ptr<int32_t>();
+    r.pool = pool;
+    r.slots = plan.slots;
+    r.kv_heads = static_cast<int32_t>(plan.kv_heads);
+    check_gk(gk_rotary_kv_store(&r, stream), "GaudiRT attention: rotary KV store");
+    q = q_rot;
+  }
   const int32_t* words = plan.storage.data_ptr<int32_t>();
   const int32_t sw = sliding_window > 0 ? static_cast<int32_t>(sliding_window) : -1;
   if (plan.prefill_seqs) {
@@ -808,6 +845,19 @@ at::Tensor paged_attn_validated(const at::Tensor& query, const at::Tensor& key, 
   return output;
 }
 
+// _paged_attn_validated (src/bridge/paged_attention.cpp:172-347).
+at::Tensor paged_attn_validated(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
+                                const at::Tensor& key_pool, const at::Tensor& value_pool, const at::Tensor& locations,
+                                const at::Tensor& requests, const at::Tensor& positions, const at::Tensor& plan_tensor,
+                                const at::Tensor& header, int64_t head_dim, double scale, double softcap,
+                                int64_t sliding_window) {
+  (void)requests;
+  (void)positions;
+  (void)header;
+  return paged_attn_impl(query, key, value, key_pool, value_pool, locations, plan_tensor, head_dim, scale, softcap,
+                         sliding_window, nullptr);
+}
+
 // paged_attn (src/bridge/generic_private_use1.cpp:277-293).
 at::Tensor paged_attn(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
                       const at::Tensor& key_pool, const at::Tensor& value_pool,
@@ -823,6 +873,152 @@ at::Tensor paged_attn(const at::Tensor& query, const at::Tensor& key, const at::
   return paged_attn_validated(query, key, value, key_pool, value_pool, metadata->row_locations(),
                               metadata->row_requests(), metadata->rotary_positions(), plan, metadata->rotary_header(),
                               head_dim, scale, softcap, sliding_window);
+}
+
+// ---------------------------------------------------------------------------
+// Rotary position embedding
+// ---------------------------------------------------------------------------
+
+// Row limit of the bucketed rotary outputs (src/bridge/bucket_program.hpp:20).
+constexpr int64_t kMaxBucketRows = 8192;
+
+// A bf16 matrix as the rotary kernel takes it: unit column stride, any row stride.
+at::Tensor rotary_rows(const at::Tensor& t) { return t.stride(1) == 1 ? t : t.contiguous(); }
+
+void launch_rotary(const at::Tensor& query, const at::Tensor& key, const at::Tensor& cache,
+                   const at::Tensor& positions, int64_t head_dim, int64_t rotary_dim, bool is_neox,
+                   const at::Tensor& q_out, const at::Tensor& k_out) {
+  const auto q = rotary_rows(query), k = rotary_rows(key);
+  gk_rotary_params p{};
+  p.struct_size = sizeof(p);
+  p.query = q.data_ptr();
+  p.q_row_stride = q.stride(0);
+  p.q_width = q.size(1);
+  p.key = k.data_ptr();
+  p.k_row_stride = k.stride(0);
+  p.k_width = k.size(1);
+  p.positions = positions.data_ptr();
+  p.positions_int64 = positions.scalar_type() == at::kLong ? 1 : 0;
+  p.cos_sin = cache.data_ptr();
+  p.cache_rows = cache.size(0);
+  p.rows = static_cast<int32_t>(q.size(0));
+  p.head_dim = static_cast<int32_t>(head_dim);
+  p.rotary_dim = static_cast<int32_t>(rotary_dim);
+  p.is_neox = is_neox ? 1 : 0;
+  p.q_out = q_out.data_ptr();
+  p.q_out_row_stride = q_out.stride(0);
+  p.k_out = k_out.data_ptr();
+  p.k_out_row_stride = k_out.stride(0);
+  check_gk(gk_rotary_embedding(&p, current_stream()), "GaudiRT rotary");
+}
+
+// Checks of src/bridge/generic_private_use1.cpp:330-353 (messages kept: the
+// reference's tests match "cache" and "rotary dimension").
+void check_rotary_inputs(const at::Tensor& query, const at::Tensor& key, const at::Tensor& cache, int64_t context,
+                         int64_t head_dim, int64_t rotary_dim) {
+  TORCH_CHECK(head_dim > 0 && head_dim <= std::numeric_limits<int32_t>::max() && rotary_dim > 0 &&
+                  rotary_dim <= head_dim && rotary_dim % 2 == 0,
+              "GaudiRT rotary: invalid head or rotary dimension");
+  const int device = current_device();
+  for (const auto& tensor : {query, key, cache})
+    TORCH_CHECK(tensor.is_cuda() && tensor.device().index() == device && tensor.scalar_type() == at::kBFloat16,
+                "GaudiRT rotary: expected BF16 device tensors");
+  TORCH_CHECK(query.dim() == 2 && key.dim() == 2 && query.size(0) > 0 && query.size(0) <= kMaxBucketRows &&
+                  key.size(0) == query.size(0) && query.size(1) > 0 && key.size(1) > 0 &&
+                  query.size(1) <= std::numeric_limits<int32_t>::max() &&
+                  key.size(1) <= std::numeric_limits<int32_t>::max() && query.size(1) % head_dim == 0 &&
+                  key.size(1) % head_dim == 0,
+              "GaudiRT rotary: invalid query or key geometry");
+  TORCH_CHECK(cache.dim() == 2 && context > 0 && cache.size(0) >= context &&
+                  cache.size(0) <= std::numeric_limits<int32_t>::max() && cache.size(1) == rotary_dim,
+              "GaudiRT rotary: cache does not cover validated positions");
+}
+
+// _rotary_embedding_validated (src/bridge/generic_private_use1.cpp:327-405):
+// positions come from validated metadata (every position < context <= cache rows).
+std::tuple<at::Tensor, at::Tensor> rotary_embedding_validated(const at::Tensor& query, const at::Tensor& key,
+                                                              const at::Tensor& cache, const at::Tensor& positions,
+                                                              const at::Tensor& header, int64_t context,
+                                                              int64_t head_dim, int64_t rotary_dim, bool is_neox) {
+  check_rotary_inputs(query, key, cache, context, head_dim, rotary_dim);
+  const auto rows = query.size(0);
+  TORCH_CHECK(positions.device() == query.device() && positions.scalar_type() == at::kInt && positions.dim() == 1 &&
+                  positions.size(0) == rows && positions.is_contiguous() && header.device() == query.device() &&
+                  header.scalar_type() == at::kInt && header.dim() == 1 && header.size(0) == 1 &&
+                  header.is_contiguous(),
+              "GaudiRT rotary: invalid validated metadata tensors");
+  const auto table = cache.contiguous();
+  auto q_out = bucket_output(query, rows, query.size(1));
+  auto k_out = bucket_output(key, rows, key.size(1));
+  launch_rotary(query, key, table, positions, head_dim, rotary_dim, is_neox, q_out, k_out);
+  return {q_out, k_out};
+}
+
+// rotary_embedding (src/bridge/generic_private_use1.cpp:407-415).
+std::tuple<at::Tensor, at::Tensor> rotary_embedding(const at::Tensor& query, const at::Tensor& key,
+                                                    const at::Tensor& cache,
+                                                    const c10::intrusive_ptr<PagedMetadata>& metadata,
+                                                    int64_t head_dim, int64_t rotary_dim, bool is_neox) {
+  TORCH_CHECK(metadata, "GaudiRT rotary: metadata is required");
+  return rotary_embedding_validated(query, key, cache, metadata->rotary_positions(), metadata->rotary_header(),
+                                    metadata->context(), head_dim, rotary_dim, is_neox);
+}
+
+// rotary_embedding_positions (src/bridge/eager_ops.cpp:1243-1300): positions
+// given directly (int32 or int64), 2-D or 3-D rows, outputs of the input shape.
+// A position outside the cache reads the nearest cache row.
+std::tuple<at::Tensor, at::Tensor> rotary_embedding_positions(const at::Tensor& query, const at::Tensor& key,
+                                                              const at::Tensor& cache, const at::Tensor& positions,
+                                                              int64_t head_dim, int64_t rotary_dim, bool is_neox) {
+  TORCH_CHECK(head_dim > 0 && head_dim <= std::numeric_limits<int32_t>::max() && rotary_dim > 0 &&
+                  rotary_dim <= head_dim && rotary_dim % 2 == 0,
+              "GaudiRT: rotary_embedding_positions invalid head_size or rotary_dim");
+  TORCH_CHECK(query.is_cuda() && key.device() == query.device() && cache.device() == query.device() &&
+                  positions.device() == query.device(),
+              "GaudiRT: rotary_embedding_positions requires same-device GPU tensors");
+  TORCH_CHECK(query.scalar_type() == at::kBFloat16 && key.scalar_type() == at::kBFloat16 &&
+                  cache.scalar_type() == at::kBFloat16 &&
+                  (positions.scalar_type() == at::kInt || positions.scalar_type() == at::kLong),
+              "GaudiRT: rotary_embedding_positions expects BF16 query/key/cache and Int32/Int64 positions");
+  TORCH_CHECK((query.dim() == 2 || query.dim() == 3) && key.dim() == query.dim() && key.size(0) == query.size(0) &&
+                  cache.dim() == 2 && cache.size(1) == rotary_dim && cache.size(0) > 0 && positions.dim() == 1 &&
+                  positions.size(0) == query.size(0),
+              "GaudiRT: rotary_embedding_positions shape mismatch");
+  if (!query.numel()) return {at::empty(query.sizes(), query.options()), at::empty(key.sizes(), key.options())};
+  const auto rows = query.size(0);
+  const auto q2 = query.reshape({rows, -1}), k2 = key.reshape({rows, -1});
+  TORCH_CHECK(q2.size(1) % head_dim == 0 && k2.size(1) % head_dim == 0 && q2.size(1) / head_dim <= 65535 &&
+                  k2.size(1) / head_dim <= 65535 && rows <= std::numeric_limits<int32_t>::max(),
+              "GaudiRT: rotary_embedding_positions shape mismatch");
+  auto q_out = at::empty(query.sizes(), query.options());
+  auto k_out = at::empty(key.sizes(), key.options());
+  launch_rotary(q2, k2, cache.contiguous(), positions.contiguous(), head_dim, rotary_dim, is_neox,
+                q_out.view({rows, -1}), k_out.view({rows, -1}));
+  return {q_out, k_out};
+}
+
+// rotary_paged_attn: the rotary embedding of a layer fused into the KV store of
+// its paged attention. Equals paged_attn(q', k', value, ...) with
+// (q', k') = rotary_embedding(query, key, cache, metadata, ...), bit for bit,
+// but the rotated keys go from registers into the pool instead of through an
+// intermediate tensor. No counterpart in the reference: there the rotary
+// recipe and the attention store are separate launches
+// (src/bridge/generic_private_use1.cpp:327-405, src/bridge/paged_attention.cpp:66-76).
+at::Tensor rotary_paged_attn(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
+                             const at::Tensor& key_pool, const at::Tensor& value_pool, const at::Tensor& cache,
+                             const c10::intrusive_ptr<PagedMetadata>& metadata, int64_t head_dim, int64_t rotary_dim,
+                             bool is_neox, double scale, double softcap, int64_t sliding_window) {
+  TORCH_CHECK(metadata, "GaudiRT paged attention: metadata is required");
+  TORCH_CHECK(query.dim() == 2 && key_pool.dim() == 3 && (head_dim == 64 || head_dim == 128 || head_dim == 256),
+              "GaudiRT paged attention: invalid tensor ranks or head dimension");
+  check_rotary_inputs(query, key, cache, metadata->context(), head_dim, rotary_dim);
+  const auto q_heads = query.size(1) / head_dim;
+  const auto kv_heads = key_pool.size(1);
+  auto plan = sliding_window > 0 ? metadata->attention_plan_for(q_heads, kv_heads, head_dim, sliding_window)
+                                 : metadata->attention_plan(q_heads, kv_heads, head_dim);
+  const RotarySpec spec{cache.contiguous(), metadata->rotary_positions(), rotary_dim, is_neox};
+  return paged_attn_impl(query, key, value, key_pool, value_pool, metadata->row_locations(), plan, head_dim, scale,
+                         softcap, sliding_window, &spec);
 }
 
 // advance_decode_lengths (src/bridge/eager_scheduler.cpp:50-82).
@@ -947,12 +1143,26 @@ TORCH_LIBRARY(gaudirt, m) {
         "Tensor locations, Tensor requests, Tensor positions, Tensor mapping, Tensor header, "
         "int head_dim, float scale, float softcap=0.0, int sliding_window=-1) -> Tensor");
   m.def("_advance_decode_lengths(Tensor seq_lens, Tensor orig_seq_lens) -> (Tensor, Tensor)");
+  m.def("rotary_embedding(Tensor query, Tensor key, Tensor cache, "
+        "__torch__.torch.classes.gaudirt.PagedMetadata metadata, int head_dim, int rotary_dim, bool is_neox) "
+        "-> (Tensor, Tensor)");
+  m.def("rotary_embedding_positions(Tensor query, Tensor key, Tensor cache, Tensor positions, "
+        "int head_dim, int rotary_dim, bool is_neox) -> (Tensor, Tensor)");
+  m.def("_rotary_embedding_validated(Tensor query, Tensor key, Tensor cache, Tensor positions, "
+        "Tensor header, int context, int head_dim, int rotary_dim, bool is_neox) -> (Tensor, Tensor)");
+  m.def("rotary_paged_attn(Tensor query, Tensor key, Tensor value, Tensor(a!) key_pool, Tensor(b!) value_pool, "
+        "Tensor cache, __torch__.torch.classes.gaudirt.PagedMetadata metadata, int head_dim, int rotary_dim, "
+        "bool is_neox, float scale, float softcap=0.0, int sliding_window=-1) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(gaudirt, CUDA, m) {
   m.impl("paged_attn", TORCH_FN(gaudirt_amd::paged_attn));
   m.impl("_paged_attn_validated", TORCH_FN(gaudirt_amd::paged_attn_validated));
   m.impl("_advance_decode_lengths", TORCH_FN(gaudirt_amd::advance_decode_lengths));
+  m.impl("rotary_embedding", TORCH_FN(gaudirt_amd::rotary_embedding));
+  m.impl("rotary_embedding_positions", TORCH_FN(gaudirt_amd::rotary_embedding_positions));
+  m.impl("_rotary_embedding_validated", TORCH_FN(gaudirt_amd::rotary_embedding_validated));
+  m.impl("rotary_paged_attn", TORCH_FN(gaudirt_amd::rotary_paged_attn));
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

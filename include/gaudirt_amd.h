@@ -177,6 +177,61 @@ int gk_advance_decode_lengths(const int64_t* seq_lens, const int32_t* orig_seq_l
                               int64_t* next, int32_t* orig_next, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Rotary position embedding of the query and key rows. Replaces the
+ * gk_rotary_bf16_v1 launch of src/bridge/generic_private_use1.cpp:294-405
+ * (rotary_embedding, _rotary_embedding_validated) and the rotary_pos bucket
+ * program of src/bridge/eager_ops.cpp:1243-1300 (rotary_embedding_positions).
+ *
+ * Every head_dim-wide head of a query or key row is rotated in its first
+ * rotary_dim elements by the cos/sin row of its position: cos_sin is bf16
+ * [cache_rows, rotary_dim], cos in the first rotary_dim / 2 columns, sin in the
+ * rest. Pairs (a, b) are (x[i], x[i + rotary_dim / 2]) with is_neox, else
+ * (x[2i], x[2i + 1]); each becomes (a cos_i - b sin_i, b cos_i + a sin_i),
+ * computed in fp32 and rounded to bf16 (round to nearest even). Elements past
+ * rotary_dim are copied. Positions are int32 (positions_int64 = 0) or int64;
+ * a position outside [0, cache_rows) reads the nearest cache row (callers
+ * validate positions; the reference's validated entry points check them on the
+ * host against the cache).
+ *
+ * gk_rotary_embedding writes q_out and k_out (rows of q_width / k_width
+ * elements). gk_rotary_kv_store is the fused write side of a layer: it writes
+ * q_out, and instead of k_out stores the rotated key rows and the value rows
+ * into the head-major KV pool at slot_mapping[r] with gk_kv_store semantics
+ * (k_width = kv_heads * head_dim, head_dim 64/128/256, 16-byte aligned rows;
+ * a negative slot skips the row). It replaces the rotary launch plus the KV
+ * store that src/bridge/paged_attention.cpp:66-76,251-263 runs on the rotated
+ * key, so the rotated key never round-trips through HBM.
+ * ------------------------------------------------------------------------- */
+typedef struct gk_rotary_params {
+  size_t struct_size;          /* sizeof(gk_rotary_params) */
+  const void* query;           /* bf16 [rows, q_width], row stride q_row_stride elements */
+  int64_t q_row_stride;
+  int64_t q_width;             /* a multiple of head_dim */
+  const void* key;             /* bf16 [rows, k_width] */
+  int64_t k_row_stride;
+  int64_t k_width;
+  const void* positions;       /* [rows] int32 or int64 */
+  int32_t positions_int64;
+  const void* cos_sin;         /* bf16 [cache_rows, rotary_dim], row-contiguous */
+  int64_t cache_rows;
+  int32_t rows, head_dim, rotary_dim, is_neox;
+  void* q_out;                 /* bf16 [rows, q_width] */
+  int64_t q_out_row_stride;
+  void* k_out;                 /* bf16 [rows, k_width]; gk_rotary_embedding only */
+  int64_t k_out_row_stride;
+  /* gk_rotary_kv_store only: */
+  const void* value;           /* bf16 [rows, kv_heads * head_dim] */
+  int64_t v_row_stride;
+  const int32_t* slot_mapping; /* [rows] */
+  void* pool;                  /* head-major pool (see the file comment) */
+  int64_t slots;
+  int32_t kv_heads;
+} gk_rotary_params;
+
+int gk_rotary_embedding(const gk_rotary_params* params, hipStream_t stream);
+int gk_rotary_kv_store(const gk_rotary_params* params, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Device metadata: normalisation and validation of device-resident scheduler
  * inputs. Replaces the gk_paged_metadata_i32_v1 / gk_scheduler_metadata_i32_v1
  * and gk_token_indices_i32_v1 / gk_scheduler_tokens_i32_v1 launches of

@@ -41,6 +41,13 @@ Parity status (how each oracle function is pinned; see tests/test_oracle.py):
 - ``page_flags`` / ``largest_page``: closed forms (identity map -> 1024, a map
   shifted by one slot -> 1, permuted pages of P -> P) and brute force over
   random block tables.
+- ``rotary_bf16``: closed forms (cos 1 / sin 0 is the identity, a quarter turn
+  maps (a, b) to (-b, a), a half turn negates), a brute force over tiny inputs
+  with Python complex products (exact in binary64, so rounding once to fp32 and
+  once to bf16 gives the fp32 reference's bits) for both pair layouts, and the
+  relative-L2 gate of tests/rotary_runtime_smoke.py:51-60 against the fp64
+  form on the reference test's shapes. ``rotary_f64`` is the fp64 form
+  (tests/rotary_runtime_smoke.py:34-48 with fp64=True).
 - ``allocate_paged_slots`` / ``release_paged_slots``: the expected values of
   tests/paged_slots_device_smoke.py (evaluated literally for P = 16 and 64),
   of tests/paged_attention_generalized_smoke.py:146-158 and
@@ -490,3 +497,73 @@ def release_paged_slots(slots, page_size, max_pages):
             seen.add(page)
             pages.append(page)
     return pages
+
+
+# ---------------------------------------------------------------------------
+# Rotary position embedding (tests/rotary_runtime_smoke.py:34-48)
+# ---------------------------------------------------------------------------
+
+def _rotary_split(x, rotary_dim, neox):
+    half = rotary_dim // 2
+    rot = x[..., :rotary_dim]
+    return (rot[..., :half], rot[..., half:]) if neox else (rot[..., 0::2], rot[..., 1::2])
+
+
+def _rotary_join(out, first, second, rotary_dim, neox):
+    half = rotary_dim // 2
+    if neox:
+        out[..., :half] = first
+        out[..., half:rotary_dim] = second
+    else:
+        out[..., 0:rotary_dim:2] = first
+        out[..., 1:rotary_dim:2] = second
+    return out
+
+
+def rotary_bf16(x_bits, cos_sin_bits, positions, head_dim, rotary_dim, neox):
+    """Rotated bf16 rows (uint16 [rows, width]) as the reference's fp32 form computes
+    them: per head, pairs (a, b) -> (bf16(a cos - b sin), bf16(b cos + a sin)) in
+    float32 with cos/sin from row ``positions[r]`` of the [cache_rows, rotary_dim]
+    table (cos | sin); elements past rotary_dim are unchanged."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows = x_bits.shape[0]
+    x = bf16_to_f32(x_bits).reshape(rows, -1, head_dim)
+    table = bf16_to_f32(cos_sin_bits)[np.asarray(positions, dtype=np.int64)]
+    half = rotary_dim // 2
+    cos, sin = table[:, None, :half], table[:, None, half:rotary_dim]
+    a, b = _rotary_split(x, rotary_dim, neox)
+    first = bf16_from_f32((a * cos - b * sin).astype(np.float32))
+    second = bf16_from_f32((b * cos + a * sin).astype(np.float32))
+    out = x_bits.reshape(rows, -1, head_dim).copy()
+    return _rotary_join(out, first, second, rotary_dim, neox).reshape(x_bits.shape)
+
+
+def rotary_f64(x_bits, cos_sin_bits, positions, head_dim, rotary_dim, neox):
+    """fp64 form: the same pairs computed in binary64 and rounded once to bf16,
+    returned as float64 values (tests/rotary_runtime_smoke.py:34-48, fp64=True)."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows = x_bits.shape[0]
+    x = bf16_to_f32(x_bits).astype(np.float64).reshape(rows, -1, head_dim)
+    table = bf16_to_f32(cos_sin_bits).astype(np.float64)[np.asarray(positions, dtype=np.int64)]
+    half = rotary_dim // 2
+    cos, sin = table[:, None, :half], table[:, None, half:rotary_dim]
+    a, b = _rotary_split(x, rotary_dim, neox)
+    first = bf16_to_f32(bf16_from_f64(a * cos - b * sin)).astype(np.float64)
+    second = bf16_to_f32(bf16_from_f64(b * cos + a * sin)).astype(np.float64)
+    out = x.copy()
+    return _rotary_join(out, first, second, rotary_dim, neox).reshape(rows, -1)
+
+
+def rotary_gate(actual_bits, x_bits, cos_sin_bits, positions, head_dim, rotary_dim, neox):
+    """The reference test's acceptance (tests/rotary_runtime_smoke.py:51-60): per-row
+    relative L2 error against the fp64 form <= max(3e-3, 2 * floor) and <= 1e-2,
+    floor = the fp32 form's own error. Returns (error, floor)."""
+    ref64 = rotary_f64(x_bits, cos_sin_bits, positions, head_dim, rotary_dim, neox)
+    ref32 = bf16_to_f32(rotary_bf16(x_bits, cos_sin_bits, positions, head_dim, rotary_dim, neox)).astype(np.float64)
+    actual = bf16_to_f32(np.asarray(actual_bits, dtype=np.uint16)).astype(np.float64).reshape(ref64.shape)
+    assert np.isfinite(actual).all() and np.isfinite(ref64).all()
+    denom = np.maximum(np.linalg.norm(ref64, axis=-1), 1e-30)
+    error = float((np.linalg.norm(actual - ref64, axis=-1) / denom).max())
+    floor = float((np.linalg.norm(ref32 - ref64, axis=-1) / denom).max())
+    assert error <= max(3e-3, 2 * floor) and error <= 1e-2, (error, floor)
+    return error, floor

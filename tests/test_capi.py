@@ -112,3 +112,30 @@ def test_metadata_and_allocator_validation(lib):
     rc = lib.gk_paged_release_slots(ctypes.c_void_p(16), 4, 16, 512, ctypes.c_void_p(16), 8, ctypes.c_void_p(16),
                                     ctypes.c_void_p(16), None)
     assert rc == capi.GK_ERR_WORKSPACE
+
+
+def test_rotary_validation(lib):
+    p = capi.RotaryParams()
+    p.struct_size = 24
+    assert lib.gk_rotary_embedding(ctypes.byref(p), None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "struct_size" in lib.gk_last_error().decode()
+    p = capi.RotaryParams()
+    p.rows, p.head_dim, p.rotary_dim, p.q_width, p.k_width, p.cache_rows = 4, 128, 127, 1024, 256, 64
+    assert lib.gk_rotary_embedding(ctypes.byref(p), None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "rotary dimension" in lib.gk_last_error().decode()
+    p.rotary_dim, p.k_width = 128, 200
+    assert lib.gk_rotary_embedding(ctypes.byref(p), None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "geometry" in lib.gk_last_error().decode()
+    p.k_width = 256
+    assert lib.gk_rotary_embedding(ctypes.byref(p), None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "null pointer" in lib.gk_last_error().decode()
+    p.rows = 0
+    assert lib.gk_rotary_embedding(ctypes.byref(p), None) == capi.GK_OK
+    # The fused store checks the pool geometry before anything is launched.
+    p.rows = 4
+    for name in ("query", "key", "positions", "cos_sin", "q_out", "value", "slot_mapping", "pool"):
+        setattr(p, name, 16)
+    p.q_row_stride, p.k_row_stride, p.q_out_row_stride, p.v_row_stride = 1024, 256, 1024, 256
+    p.slots, p.kv_heads = 128, 1
+    assert lib.gk_rotary_kv_store(ctypes.byref(p), None) == capi.GK_ERR_INVALID_ARGUMENT
+    assert "pool geometry" in lib.gk_last_error().decode()  # k_width != kv_heads * head_dim

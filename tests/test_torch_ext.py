@@ -21,6 +21,16 @@ SCHEMAS = {
                              "float softcap=0.0, int sliding_window=-1) -> Tensor",
     "_advance_decode_lengths": "gaudirt::_advance_decode_lengths(Tensor seq_lens, Tensor orig_seq_lens) "
                                "-> (Tensor, Tensor)",
+    # src/bridge/generic_private_use1.cpp:464-470
+    "rotary_embedding": "gaudirt::rotary_embedding(Tensor query, Tensor key, Tensor cache, "
+                        "__torch__.torch.classes.gaudirt.PagedMetadata metadata, int head_dim, int rotary_dim, "
+                        "bool is_neox) -> (Tensor, Tensor)",
+    "rotary_embedding_positions": "gaudirt::rotary_embedding_positions(Tensor query, Tensor key, Tensor cache, "
+                                  "Tensor positions, int head_dim, int rotary_dim, bool is_neox) "
+                                  "-> (Tensor, Tensor)",
+    "_rotary_embedding_validated": "gaudirt::_rotary_embedding_validated(Tensor query, Tensor key, Tensor cache, "
+                                   "Tensor positions, Tensor header, int context, int head_dim, int rotary_dim, "
+                                   "bool is_neox) -> (Tensor, Tensor)",
 }
 
 
@@ -155,3 +165,26 @@ def test_slot_allocator_rejects_host_tensors(ext):
         ext._allocate_paged_slots(last, torch.arange(4), [0], [3], 16)
     with pytest.raises(RuntimeError, match="GaudiRT"):
         ext._release_paged_slots(last, 16, 512)
+
+
+def test_rotary_fake_kernels_trace():
+    # torch.compile traces the rotary ops (and the fused attention) through the
+    # registered fake kernels; no device work happens under FakeTensorMode.
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(5, 4 * 128, dtype=torch.bfloat16)
+        k = torch.empty(5, 2 * 128, dtype=torch.bfloat16)
+        cache = torch.empty(64, 128, dtype=torch.bfloat16)
+        pos = torch.empty(5, dtype=torch.int32)
+        qo, ko = torch.ops.gaudirt.rotary_embedding_positions(q, k, cache, pos, 128, 128, True)
+        assert qo.shape == q.shape and ko.shape == k.shape and qo.dtype == torch.bfloat16
+        qo, ko = torch.ops.gaudirt._rotary_embedding_validated(q, k, cache, pos, torch.empty(1, dtype=torch.int32),
+                                                               64, 128, 128, False)
+        assert qo.shape == q.shape and ko.shape == k.shape
+
+
+def test_rotary_paged_attn_schema():
+    # The fused op (no reference counterpart) takes paged_attn's arguments plus the rotary ones.
+    schema = str(torch.ops.gaudirt.rotary_paged_attn.default._schema)
+    assert "Tensor(a!) key_pool" in schema and "Tensor cache" in schema and "int rotary_dim" in schema
