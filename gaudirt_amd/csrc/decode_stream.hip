@@ -333,8 +333,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   };
 
   auto finalize = [&](const TileDesc& t) {
-    l_run += shfl_xor(l_run, 16);
-    l_run += shfl_xor(l_run, 32);
+    l_run = col4_sum(l_run);
     float lrow[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -437,8 +436,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
         sc[h][r] = s;
         mx = fmaxf(mx, s);
       }
-    mx = fmaxf(mx, shfl_xor(mx, 16));
-    mx = fmaxf(mx, shfl_xor(mx, 32));
+    mx = col4_max(mx);
     if (__builtin_amdgcn_ballot_w64(mx > m_run + kDecodeLazyRescale)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);

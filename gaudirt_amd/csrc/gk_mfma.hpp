@@ -48,6 +48,25 @@ __device__ __forceinline__ int swz(int t, int cpr) {
   return cpr >= 16 ? (((t & 7) << 1) | ((t >> 3) & 1)) : (((t & 3) << 1) | ((t >> 2) & 1));
 }
 
+// Max / sum over the four lanes c, c + 16, c + 32, c + 48 of a column of the
+// 16-lane rows, with gfx950's cross-row swaps instead of LDS permutes.
+// permlane32_swap(x, x) leaves, in every lane l, x[l % 32] in the first result
+// and x[l % 32 + 32] in the second; permlane16_swap does the same for rows
+// (0, 1) and (2, 3). Both orders of each addition give the same float, so every
+// lane of the column ends with the same value.
+__device__ __forceinline__ float col4_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col4_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Wait until at most N vector memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmem() {

@@ -224,8 +224,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
         sc[h][r] = s;
         mx = fmaxf(mx, s);
       }
-    mx = fmaxf(mx, shfl_xor(mx, 16));
-    mx = fmaxf(mx, shfl_xor(mx, 32));
+    mx = col4_max(mx);
     if (__builtin_amdgcn_ballot_w64(mx > m_run + kDecodeLazyRescale)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
@@ -324,8 +323,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
   }
 
   // Per-head sums over the four lane groups; m_run is already uniform per head.
-  l_run += shfl_xor(l_run, 16);
-  l_run += shfl_xor(l_run, 32);
+  l_run = col4_sum(l_run);
   // o rows are heads 4q + r: fetch each row's sum from lane c16 == 4q + r.
   float lrow[4];
 #pragma unroll

@@ -193,36 +193,43 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
     }
 
     // A step whose keys every valid query row of this wave sees (below the
-    // causal diagonal, inside the window) needs no per-element mask, and its
-    // scale folds into the exponent (max of raw scores times scale > 0, then
-    // exp2(fma(s, scale, -max))): a third of the softmax instructions.
+    // causal diagonal, inside the window) needs no per-element mask. Without
+    // softcap the scale folds into the exponent: masked scores become -inf in
+    // place (the same registers on both paths), the row maximum is taken on raw
+    // scores (scale > 0), and p = exp2(fma(s, scale, -max)).
     const bool full = !SOFTCAP && tb + kKeys - 1 <= wave_pos_min && tb >= wave_left_max;
     bf16x8_t pa[kNT];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
       float mx = -INFINITY;
-      if (full) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[h][nt][r]);
-        mx *= a.score_scale;
-      } else {
+      if constexpr (SOFTCAP) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int key = tb + 16 * h + 4 * q + r;
-            float s;
-            if constexpr (SOFTCAP) s = a.softcap_log2 * soft_tanh(sc[h][nt][r] * a.score_scale);
-            else s = sc[h][nt][r] * a.score_scale;
+            float s = a.softcap_log2 * soft_tanh(sc[h][nt][r] * a.score_scale);
             s = (key <= qpos[nt] && key >= qleft[nt]) ? s : -INFINITY;
             sc[h][nt][r] = s;
             mx = fmaxf(mx, s);
           }
+      } else {
+        if (!full) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = tb + 16 * h + 4 * q + r;
+              sc[h][nt][r] = (key <= qpos[nt] && key >= qleft[nt]) ? sc[h][nt][r] : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[h][nt][r]);
+        mx *= a.score_scale;
       }
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
+      mx = col4_max(mx);
       if (__builtin_amdgcn_ballot_w64(mx > m_run[nt] + kLazyRescale)) {
         const float m_new = fmaxf(m_run[nt], mx);
         const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
@@ -238,12 +245,10 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       }
       const float base = m_run[nt] == -INFINITY ? 0.f : m_run[nt];
       float ps[8];
-      if (full) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ps[i] = fast_exp2(sc[i >> 2][nt][i & 3] - base);
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (SOFTCAP) ps[i] = fast_exp2(sc[i >> 2][nt][i & 3] - base);
+        else ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -298,9 +303,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   // Per-qrow sums over the four lane groups, then normalise and store.
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
-    float l = l_run[nt];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    const float l = col4_sum(l_run[nt]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       // o row 4q + r of tile nt; its sum lives in lane c16 == 4q + r.
