@@ -92,20 +92,34 @@ struct Cursor {
   int next_ctx, next_req, next_qrow;  // row + 1, fetched ahead
 };
 
-// What consuming one tile needs (wave-uniform).
+// What consuming one tile needs (wave-uniform). The tile's keys fall into NR
+// runs of TS / NR keys, each inside one pool block: one run when blocks hold
+// at least TS keys, one run per 16-byte load of the tile otherwise.
+template <int NR>
 struct TileDesc {
   int tb;                   // first key of the tile
   int left, ctx;            // visible keys of the row
   int row, h, kvh, j, count, qrow;
   int64_t g;
-  uint32_t row0;            // byte offset of key tb in its kv head's K (and V) region
+  uint32_t row0[NR];        // byte offset of run i's first key in its kv head's K (and V) region
   int q_start, q_end;       // first / last tile of the unit in this workgroup
 };
 
-template <int D, bool SOFTCAP>
+// Block-table entries of one tile's runs.
+template <int NR>
+struct TileEntries {
+  int e[NR];
+};
+
+// SMALL: pool blocks shorter than a tile (but at least one load's TS / LOADS
+// keys); each load of a tile then reads its own block-table entry.
+template <int D, bool SOFTCAP, bool SMALL>
 __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   using S = MfmaShape<D>;
   constexpr int TS = S::TS;
+  constexpr int NR = SMALL ? S::LOADS : 1;  // key runs of a tile
+  constexpr int KPR = TS / NR;              // keys of one run
+  using TileDesc = gk::TileDesc<NR>;
   constexpr int QBYTES = 16 * D * 2;  // one unit's query heads (up to 16)
   // Two K/V stages, each tile its own LDS object so that the compiler tells
   // reads of one from the direct loads in flight into another, and the two
@@ -224,12 +238,23 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     if (p >= c.rt.count) p -= c.rt.count;
     return (c.rt.first + p) * TS;
   };
-  // Block-table entry of the cursor's tile (a scalar load, issued ahead of use).
+  // Block-table entries of the cursor's tile (scalar loads, issued ahead of use).
+  // A run wholly outside the visible keys takes the entry of the nearest
+  // visible key instead, so that only blocks the row owns are read; its keys
+  // are masked. An empty row's masked tile reads no table entry.
   auto table_entry = [&](const Cursor& c) {
-    // An empty row's masked tile reads no table entry.
-    return c.rt.ctx > 0 ? scalar_load(a.block_tables, (int64_t)c.req * a.bt_stride + (tile_key(c) >> shift)) : 0;
+    TileEntries<NR> r;
+    const int tb = tile_key(c);
+    const int64_t bt_row = (int64_t)c.req * a.bt_stride;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      int key = tb + i * KPR;
+      if constexpr (SMALL) key = min(max(key, c.rt.left), c.rt.ctx - 1);
+      r.e[i] = c.rt.ctx > 0 ? scalar_load(a.block_tables, bt_row + (key >> shift)) : 0;
+    }
+    return r;
   };
-  auto describe = [&](const Cursor& c, int entry) {
+  auto describe = [&](const Cursor& c, const TileEntries<NR>& en) {
     TileDesc t;
     t.tb = tile_key(c);
     t.left = c.rt.left;
@@ -241,7 +266,9 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     t.count = c.rt.count;
     t.qrow = c.qrow;
     t.g = c.g;
-    t.row0 = (((uint32_t)entry << shift) | (uint32_t)(t.tb & block_mask)) * (uint32_t)(2 * D);
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+      t.row0[i] = (((uint32_t)en.e[i] << shift) | (uint32_t)((t.tb + i * KPR) & block_mask)) * (uint32_t)(2 * D);
     t.q_start = c.j == 0 || c.g == g_begin;
     t.q_end = c.j == c.rt.count - 1 || c.g == g_end - 1;
     return t;
@@ -260,12 +287,14 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
-      lds_dma16(kl + i * 1024, krs, t.row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4));
+      const uint32_t row = SMALL ? t.row0[i] + (tt - i * KPR) * (2 * D) : t.row0[0] + tt * (2 * D);
+      lds_dma16(kl + i * 1024, krs, row + ((pc ^ swz(tt, D / 8)) << 4));
     }
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
-      lds_dma16(vl + i * 1024, vrs, t.row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4));
+      const uint32_t row = SMALL ? t.row0[i] + (tt - i * KPR) * (2 * D) : t.row0[0] + tt * (2 * D);
+      lds_dma16(vl + i * 1024, vrs, row + ((pc ^ swz(tt, D / 8)) << 4));
     }
   };
   // The unit's query heads -> LDS ([head][D], row-major). The resource covers
@@ -514,7 +543,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   if (d0.q_start) issue_query(d0, qs[0]);
   issue_tile(d0, kt0, vt0);
   --to_issue;
-  int next_entry = 0;
+  TileEntries<NR> next_entry = {};
   if (to_issue > 0) {
     advance(cur);
     next_entry = table_entry(cur);
@@ -631,19 +660,24 @@ __global__ __launch_bounds__(64) void stream_merge_kernel(StreamMergeArgs m) {
   for (int e = 0; e < PER_LANE; ++e) dst[lane + 64 * e] = (uint16_t)bf16_bits(acc[e] * inv);
 }
 
-template <int D, bool SOFTCAP>
+template <int D, bool SOFTCAP, bool SMALL>
 int resident_per_cu() {
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<D, SOFTCAP>, 64, 0) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<D, SOFTCAP, SMALL>, 64, 0) !=
+          hipSuccess ||
       n <= 0)
     n = 1;
   return n;
 }
 
 template <int D>
-int resident_per_cu(bool softcap) {
-  return softcap ? resident_per_cu<D, true>() : resident_per_cu<D, false>();
+int resident_per_cu(bool softcap, bool small) {
+  if (small) return softcap ? resident_per_cu<D, true, true>() : resident_per_cu<D, false, true>();
+  return softcap ? resident_per_cu<D, true, false>() : resident_per_cu<D, false, false>();
 }
+
+// Blocks shorter than a tile take the per-load block-table variant.
+bool small_blocks(int head_dim, int block_size) { return block_size < (head_dim == 256 ? 16 : 32); }
 
 }  // namespace
 
@@ -651,20 +685,21 @@ int device_cus();
 
 // Workgroups of the balanced grid: the CUs times the workgroups one CU keeps
 // resident (LDS-bound), queried once per device and kernel variant.
-int stream_decode_wgs(int head_dim, bool softcap) {
+int stream_decode_wgs(int head_dim, bool softcap, int block_size) {
   static std::mutex mu;
-  static int cached[64][3][2] = {};
+  static int cached[64][3][2][2] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   const int di = head_dim == 64 ? 0 : (head_dim == 128 ? 1 : 2);
+  const bool small = small_blocks(head_dim, block_size);
   std::lock_guard<std::mutex> lock(mu);
-  int& slot = cached[dev][di][softcap ? 1 : 0];
+  int& slot = cached[dev][di][softcap ? 1 : 0][small ? 1 : 0];
   if (!slot) {
     int per_cu = 1;
     switch (head_dim) {
-      case 64: per_cu = resident_per_cu<64>(softcap); break;
-      case 128: per_cu = resident_per_cu<128>(softcap); break;
-      default: per_cu = resident_per_cu<256>(softcap); break;
+      case 64: per_cu = resident_per_cu<64>(softcap, small); break;
+      case 128: per_cu = resident_per_cu<128>(softcap, small); break;
+      default: per_cu = resident_per_cu<256>(softcap, small); break;
     }
     slot = device_cus() * per_cu;
   }
@@ -692,9 +727,15 @@ int launch_stream_decode(const DecodeArgs& a, bool softcap, int head_dim, int wg
   sa.unit_span = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes + ml_bytes);
 
   const dim3 grid(wgs);
+  const bool small = small_blocks(head_dim, 1 << a.block_shift);
 #define GK_STREAM_LAUNCH(D)                                                                      \
-  if (softcap) decode_stream_kernel<D, true><<<grid, 64, 0, stream>>>(sa);                       \
-  else decode_stream_kernel<D, false><<<grid, 64, 0, stream>>>(sa);
+  if (small) {                                                                                   \
+    if (softcap) decode_stream_kernel<D, true, true><<<grid, 64, 0, stream>>>(sa);               \
+    else decode_stream_kernel<D, false, true><<<grid, 64, 0, stream>>>(sa);                      \
+  } else {                                                                                       \
+    if (softcap) decode_stream_kernel<D, true, false><<<grid, 64, 0, stream>>>(sa);              \
+    else decode_stream_kernel<D, false, false><<<grid, 64, 0, stream>>>(sa);                     \
+  }
   switch (head_dim) {
     case 64: GK_STREAM_LAUNCH(64) break;
     case 128: GK_STREAM_LAUNCH(128) break;

@@ -723,13 +723,13 @@ int device_cus() {
 //    length max_context / 2) fits the resident waves, else 1024.
 // dot2 path: halve a 2048-key partition until the items fill the GPU.
 // The balanced schedule (decode_stream.hip) serves the MFMA path whenever the
-// caller leaves the partition to the library and every TS-key tile lies in one
-// pool block; an explicit partition, small blocks and small groups take the
-// partitioned kernels.
+// caller leaves the partition to the library and the keys one 16-byte load
+// per lane covers (64 / (head_dim / 8)) lie in one pool block; an explicit
+// partition, smaller blocks and small groups take the partitioned kernels.
 bool use_stream(const gk_decode_params* p) {
   const int group = p->q_heads / p->kv_heads;
-  const int ts = p->head_dim == 256 ? 16 : 32;
-  return p->partition_tokens == 0 && use_mfma(group) && p->block_size >= ts;
+  const int keys_per_load = 64 / (p->head_dim / 8);
+  return p->partition_tokens == 0 && use_mfma(group) && p->block_size >= keys_per_load;
 }
 
 int32_t decode_partition(const gk_decode_params* p) {
@@ -770,7 +770,7 @@ int64_t stream_units(const gk_decode_params* p) {
 size_t decode_workspace_bytes(const gk_decode_params* p) {
   if (p->rows > 0 && use_stream(p))
     return stream_decode_workspace_bytes(p->head_dim, heads_per_workgroup(p->q_heads / p->kv_heads), stream_units(p),
-                                         stream_decode_wgs(p->head_dim, p->softcap > 0.f));
+                                         stream_decode_wgs(p->head_dim, p->softcap > 0.f, p->block_size));
   const int32_t parts = decode_max_parts(p);
   if (parts <= 1 || p->rows == 0) return 0;
   const size_t n = (size_t)p->rows * p->q_heads * parts;
@@ -822,7 +822,8 @@ int paged_decode(const gk_decode_params* p, void* workspace, size_t workspace_by
   a.out = static_cast<uint16_t*>(p->out);
   a.out_stride = p->out_row_stride;
   if (use_stream(p))
-    return launch_stream_decode(a, softcap, p->head_dim, stream_decode_wgs(p->head_dim, softcap), workspace, stream);
+    return launch_stream_decode(a, softcap, p->head_dim, stream_decode_wgs(p->head_dim, softcap, p->block_size), workspace,
+                                stream);
   if (need) {
     const size_t n = (size_t)p->rows * p->q_heads * max_parts;
     const size_t o_bytes = (n * p->head_dim * sizeof(float) + 255) & ~size_t{255};

@@ -1,7 +1,8 @@
 """GPU parity of the balanced decode schedule (gk_paged_decode with partition_tokens = 0).
 
 With the partition left to the library, GQA groups >= 4 and block_size >= the
-kernel's 32-key tile (16 for head_dim 256), gk_paged_decode splits the batch's
+keys of one 16-byte load per lane (4 for head_dim 128, 8 for 64, 2 for 256),
+gk_paged_decode splits the batch's
 key tiles evenly over one resident grid: work units (row, kv head) are cut at
 arbitrary tiles, partial states are merged with the log-sum-exp rule, and the
 tiles of a unit are visited in rotated order. These cases pin every piece of
@@ -76,6 +77,59 @@ def test_stream_block_sizes(runner, block_size):
     lens = np.array([5, 300, 777, 1024, 63, 2048, 1])
     case = cases.decode_case(block_size + 3, len(lens), 32, 8, 128, block_size, 8192 // block_size * 2, lens)
     check(case, runner.run_case(case))
+
+
+@pytest.mark.parametrize("geometry", [(128, 4), (128, 8), (128, 16), (64, 8), (64, 16), (256, 2), (256, 4),
+                                      (256, 8)])
+def test_stream_small_blocks(runner, geometry):
+    # Blocks shorter than a tile: every 16-byte load of a tile (64 / (d / 8)
+    # keys) reads its own block-table entry.
+    d, block = geometry
+    heads, kv_heads = (16, 2) if d == 256 else (32, 8)
+    lens = np.array([1, 2, 3, 4, 5, 31, 33, 300, 777, 1024, 2047])
+    case = cases.decode_case(7 * block + d, len(lens), heads, kv_heads, d, block, 8192 // block * 2, lens)
+    print("head_dim", d, "block", block, flush=True)
+    check(case, runner.run_case(case))
+
+
+@pytest.mark.parametrize("block", [4, 16])
+def test_stream_small_blocks_window_evicted(runner, block):
+    # Sliding window over blocks shorter than a tile, with every slot outside
+    # the visible keys poisoned (NaN) and the table entries of blocks wholly
+    # below the window set to -1, as after eviction: a tile's masked runs must
+    # read only blocks the row still owns.
+    import copy
+
+    lens = np.array([40, 300, 1000, 64, 65, 3000, 1, 77, 78, 79])
+    case = cases.decode_case(33 + block, len(lens), 16, 4, 128, block, 16384 // block, lens)
+    case.window, case.softcap = 77, 30.0
+    used = np.zeros(case.slots, dtype=bool)
+    evicted = case.block_tables.copy()
+    for b, n in enumerate(case.lens):
+        left = max(0, int(n) - case.window)
+        for t in range(left, n):
+            used[case.block_tables[b, t // block] * block + t % block] = True
+        evicted[b, :left // block] = -1
+    case.pool[:, :, ~used, :] = 0x7fc0
+    reference = copy.copy(case)
+    case.block_tables = evicted
+    print("block", block, flush=True)
+    check(reference, runner.run_case(case), fp32_softmax=True)
+
+
+def test_library_choice_small_blocks(runner):
+    import ctypes
+    import torch
+    from gaudirt_amd import capi
+
+    lib = capi.load()
+    for d, block, stream in [(128, 4, True), (128, 2, False), (64, 8, True), (64, 4, False), (256, 2, True),
+                             (256, 1, False)]:
+        case = cases.decode_case(1, 2, 16, 2, d, block, 256, [30, 60])
+        params = runner.decode_params(runner.bf16_device(case.query), runner.bf16_device(case.pool),
+                                      runner.to_device(case.block_tables), runner.to_device(case.lens), 16, 2, d,
+                                      block, case.scale, torch.empty(2, 16 * d, dtype=torch.bfloat16, device="cuda"))
+        assert (lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0) == stream, (d, block)
 
 
 def test_one_long_row_split_over_the_grid(runner):
