@@ -53,12 +53,19 @@ __device__ __forceinline__ int swz(int t, int cpr) {
 // permlane32_swap(x, x) leaves, in every lane l, x[l % 32] in the first result
 // and x[l % 32 + 32] in the second; permlane16_swap does the same for rows
 // (0, 1) and (2, 3). Both orders of each addition give the same float, so every
-// lane of the column ends with the same value.
+// lane of the column ends with the same value. The max is a bare v_max_f32:
+// fmaxf would first quiet both swapped operands (two more instructions), and
+// the inputs are never NaN (masked scores are -inf).
+__device__ __forceinline__ float max2(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ float col4_max(float x) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = max2(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return max2(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float col4_sum(float x) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

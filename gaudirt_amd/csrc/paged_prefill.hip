@@ -22,7 +22,8 @@
 // Numerics versus the reference (the tile chain of
 // src/bridge/paged_attention_tiles.cpp:57-195): fp32 scores times scale,
 // probabilities rounded to bf16 before P.V (relative to the running maximum),
-// fp32 accumulation, one normalisation at the end, bf16 output.
+// fp32 accumulation, one normalisation at the end by the sum of those bf16
+// probabilities, bf16 output.
 #include "gk_mfma.hpp"
 
 #include <algorithm>
@@ -130,13 +131,16 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       a.window > 0 ? pos_lo + min(nr - 1, (wave * kQrowsPerWave + kQrowsPerWave - 1) / g) - a.window + 1 : 0;
 
   f32x4_t o[kNT][S::NO];
-  float m_run[kNT], l_run[kNT];
+  // Row sums of the bf16 probabilities, in the output layout (rows 4q + r),
+  // accumulated by one more MFMA per step against an all-ones operand.
+  float m_run[kNT];
+  f32x4_t l_run[kNT];
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
 #pragma unroll
     for (int c = 0; c < S::NO; ++c) o[nt][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     m_run[nt] = -INFINITY;
-    l_run[nt] = 0.f;
+    l_run[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
   const uint16_t* kbase = a.pool + (int64_t)kvh * a.slots * D;
@@ -192,6 +196,19 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       }
     }
 
+    // V operands of P . V (keys 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2), dims
+    // 16c + 4 (c16 & 3), read transposed), all issued before the softmax so
+    // that its arithmetic covers their LDS latency.
+    bf16x8_t vb[S::NO];
+#pragma unroll
+    for (int c = 0; c < S::NO; ++c) {
+      const int lc = 2 * c + ((c16 & 3) >> 1);
+      const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
+      const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3));
+      const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3));
+      vb[c] = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+
     // A step whose keys every valid query row of this wave sees (below the
     // causal diagonal, inside the window) needs no per-element mask. Without
     // softcap the scale folds into the exponent: masked scores become -inf in
@@ -233,7 +250,6 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       if (__builtin_amdgcn_ballot_w64(mx > m_run[nt] + kLazyRescale)) {
         const float m_new = fmaxf(m_run[nt], mx);
         const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
-        l_run[nt] *= alpha;
         m_run[nt] = m_new;
         // o rows are qrows 4q + r; qrow h's factor lives in lanes with c16 == h.
 #pragma unroll
@@ -241,6 +257,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
           const float f = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(alpha)));
 #pragma unroll
           for (int c = 0; c < S::NO; ++c) o[nt][c][r] *= f;
+          l_run[nt][r] *= f;
         }
       }
       const float base = m_run[nt] == -INFINITY ? 0.f : m_run[nt];
@@ -251,24 +268,18 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
         else ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        l_run[nt] += ps[i];
-        pa[nt][i] = (__bf16)ps[i];
-      }
+      for (int i = 0; i < 8; ++i) pa[nt][i] = (__bf16)ps[i];
     }
 
-    // O[qrow][dim] += P . V: keys 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2),
-    // dims 16c + 4 (c16 & 3), read transposed.
+    // O[qrow][dim] += P . V, and the row sums.
 #pragma unroll
-    for (int c = 0; c < S::NO; ++c) {
-      const int lc = 2 * c + ((c16 & 3) >> 1);
-      const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
-      const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3));
-      const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3));
-      const bf16x8_t vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+    for (int c = 0; c < S::NO; ++c)
 #pragma unroll
-      for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[nt], vb, o[nt][c]);
-    }
+      for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[nt], vb[c], o[nt][c]);
+    const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
+                           (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) l_run[nt] = mfma32(pa[nt], ones, l_run[nt]);
   };
 
   // kStages-deep pipeline over the workgroup, one barrier per step: before it
@@ -300,14 +311,12 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
     consume(kb0 + step * kKeys, kv[cur][0], kv[cur][1]);
   }
 
-  // Per-qrow sums over the four lane groups, then normalise and store.
+  // Normalise and store: o row 4q + r of tile nt, its sum in l_run[nt][r].
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
-    const float l = col4_sum(l_run[nt]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      // o row 4q + r of tile nt; its sum lives in lane c16 == 4q + r.
-      const float lr = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l)));
+      const float lr = l_run[nt][r];
       const int qr = wave * kQrowsPerWave + nt * 16 + 4 * q + r;
       const int row = qr / g, head = qr % g;
       if (row >= nr) continue;
