@@ -77,9 +77,14 @@ struct PrefillShape {
   static constexpr int NI = TILE / 1024;            // 1 KiB load instructions per tile
 };
 
-template <int D, bool SOFTCAP>
+// SMALL: pool blocks shorter than a step's 32 keys (but at least one load's
+// 64 / (D / 8) keys); each load of a step then reads its own block-table entry.
+template <int D, bool SOFTCAP, bool SMALL>
 __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_kernel(PrefillArgs a) {
   using S = PrefillShape<D>;
+  constexpr int LPW = S::NI / kPrefillWaves;  // load instructions per wave per K (or V) tile
+  constexpr int NE = SMALL ? LPW : 1;         // block-table entries per wave per step
+  constexpr int KPL = kKeys / S::NI;          // keys of one load instruction
   // kStages K/V stages. The direct loads are asm statements the compiler does
   // not track, so one array serves every stage; reads are ordered by the
   // explicit vmcnt wait and the barrier of each step.
@@ -150,33 +155,56 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, region, kBufferDword3);
   const int shift = a.block_shift, bmask = (1 << shift) - 1;
 
-  // Direct loads of the 32-key step at tb into one stage. Steps are 32-aligned
-  // and blocks hold >= 32 keys, so a step lies in one block: its slots are
-  // consecutive from the block's slot for tb (one scalar block-table read).
-  // Piece p = 64 (LOADS * wave + i) + lane: token p / CPR, stored chunk
-  // p % CPR holding the token's chunk (p % CPR) ^ swz(token, D / 8).
-  auto issue = [&](int tb, int entry, char* kt, char* vt) {
-    const uint32_t row0 = (uint32_t)((entry << shift) | (tb & bmask)) * (2 * D);
+  // Direct loads of the 32-key step at tb into one stage. Steps are 32-aligned.
+  // Blocks of >= 32 keys hold a whole step: its slots are consecutive from the
+  // block's slot for tb (one scalar block-table read). Shorter blocks (SMALL)
+  // hold whole load instructions (KPL keys each): each of this wave's loads
+  // reads its own entry.
+  // Piece p = 64 ins + lane of load instruction ins (wave ins % waves): token
+  // p / CPR, stored chunk p % CPR holding the token's chunk (p % CPR) ^
+  // swz(token, D / 8).
+  struct Entries {
+    int e[NE];
+  };
+  auto issue = [&](int tb, const Entries& en, char* kt, char* vt) {
     const uint32_t kl = lds_addr(kt), vl = lds_addr(vt);
-    // Load instruction ins (wave ins % waves) fills 1 KiB piece ins of a tile.
 #pragma unroll
-    for (int k = 0; k < (S::NI + kPrefillWaves - 1) / kPrefillWaves; ++k) {
+    for (int k = 0; k < LPW; ++k) {
       const int ins = wave + k * kPrefillWaves;
-      if (ins >= S::NI) break;
       const int p = ins * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
-      lds_dma16(kl + ins * 1024, krs, row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4));
-      lds_dma16(vl + ins * 1024, vrs, row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4));
+      const int run = SMALL ? ins * KPL : 0;  // first key of the entry's run, relative to tb
+      const uint32_t row0 = (uint32_t)((en.e[SMALL ? k : 0] << shift) | ((tb + run) & bmask)) * (2 * D);
+      const uint32_t off = row0 + (tt - run) * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4);
+      lds_dma16(kl + ins * 1024, krs, off);
+      lds_dma16(vl + ins * 1024, vrs, off);
     }
   };
-  // Block-table entry of the step at key tb (scalar load, fetched a step ahead).
-  auto entry_of = [&](int tb) { return scalar_load(bt, tb >> shift); };
+  // Block-table entries of the step at key tb (scalar loads, fetched a step
+  // ahead). A run wholly outside the keys [key_begin, key_end) takes the
+  // entry of the nearest such key, so that only blocks the request owns are
+  // read; its keys are masked (and their V rows zeroed).
+  auto entry_of = [&](int tb) {
+    Entries en;
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      int key = tb + (SMALL ? (wave + k * kPrefillWaves) * KPL : 0);
+      if constexpr (SMALL) key = min(max(key, key_begin), key_end - 1);
+      en.e[k] = scalar_load(bt, key >> shift);
+    }
+    return en;
+  };
 
   auto consume = [&](int tb, const char* kt, char* vt) {
-    if (tb + kKeys > key_end) {
-      // Keys past the tile's last row hold arbitrary pool data: zero their V
-      // rows so that a zero probability cannot meet a non-finite value.
-      for (int p = tid; p < kKeys * S::CPR; p += kPrefillWaves * 64)
-        if (tb + p / S::CPR >= key_end) *reinterpret_cast<uint4*>(vt + p * 16) = make_uint4(0, 0, 0, 0);
+    if (tb + kKeys > key_end || (SMALL && tb < key_begin)) {
+      // Keys past the tile's last row (and, with short blocks, keys before the
+      // window's first, read from the nearest owned block) hold arbitrary pool
+      // data: zero their V rows so that a zero probability cannot meet a
+      // non-finite value. Whole-block keys before the window are stored tokens.
+      for (int p = tid; p < kKeys * S::CPR; p += kPrefillWaves * 64) {
+        const int key = tb + p / S::CPR;
+        if (key >= key_end || (SMALL && key < key_begin))
+          *reinterpret_cast<uint4*>(vt + p * 16) = make_uint4(0, 0, 0, 0);
+      }
       __syncthreads();
     }
     // S^T = K.Q^T: lane (q, c16) gets qrow c16 (+16 nt), keys tb + 16h + 4q + r.
@@ -289,7 +317,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   // step, whose buffer is refilled with the step kStages - 1 ahead.
   constexpr int LPS = 2 * S::NI / kPrefillWaves;  // direct loads per wave per stage
   static_assert(S::NI % kPrefillWaves == 0, "tile pieces split evenly over the waves");
-  int e_next = 0;
+  Entries e_next{};
 #pragma unroll
   for (int st = 0; st < kStages - 1; ++st) {
     if (st < nsteps) issue(kb0 + st * kKeys, entry_of(kb0 + st * kKeys), kv[st][0], kv[st][1]);
@@ -329,9 +357,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
 }
 
 template <int D>
-void launch(const PrefillArgs& a, bool softcap, dim3 grid, hipStream_t stream) {
-  if (softcap) prefill_kernel<D, true><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
-  else prefill_kernel<D, false><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+void launch(const PrefillArgs& a, bool softcap, bool small, dim3 grid, hipStream_t stream) {
+  if (small) {
+    if (softcap) prefill_kernel<D, true, true><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+    else prefill_kernel<D, false, true><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+  } else {
+    if (softcap) prefill_kernel<D, true, false><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+    else prefill_kernel<D, false, false><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+  }
 }
 
 }  // namespace
@@ -344,8 +377,11 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
     return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: head dimension must be 64 or 128");
   if (p->q_heads <= 0 || p->kv_heads <= 0 || p->q_heads % p->kv_heads || p->q_heads / p->kv_heads > kQrows)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: invalid head geometry (GQA group at most 128)");
-  if (!is_pow2(p->block_size) || p->block_size < kKeys || p->block_size > (1 << 20))
-    return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: block_size must be a power of two of at least 32");
+  // One load instruction covers 64 / (head_dim / 8) keys: 4 at 128, 8 at 64.
+  const int min_block = 64 / (p->head_dim / 8);
+  if (!is_pow2(p->block_size) || p->block_size < min_block || p->block_size > (1 << 20))
+    return fail(GK_ERR_UNSUPPORTED,
+                "gk_paged_prefill: block_size must be a power of two of at least 4 (head_dim 128) or 8 (64)");
   if (p->seqs < 0 || p->seqs > 65535 || p->max_rows < 0 || p->slots <= 0)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: sequence count, rows or slots out of range");
   if (p->slots > (int64_t)(UINT32_MAX / 2) / p->head_dim)
@@ -387,8 +423,9 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
   const int64_t items = (int64_t)a.tiles * p->kv_heads * p->seqs;
   if (items > (int64_t)1 << 30) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: too many rows");
   const dim3 grid((unsigned)items);
-  if (p->head_dim == 64) launch<64>(a, softcap, grid, stream);
-  else launch<128>(a, softcap, grid, stream);
+  const bool small = p->block_size < kKeys;
+  if (p->head_dim == 64) launch<64>(a, softcap, small, grid, stream);
+  else launch<128>(a, softcap, small, grid, stream);
   return hip_status(hipGetLastError(), "gk_paged_prefill launch");
 }
 

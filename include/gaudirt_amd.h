@@ -88,9 +88,10 @@ typedef struct gk_decode_params {
   int32_t sliding_window;      /* <= 0 = off */
   int32_t max_context;         /* host bound: row_context[r] <= max_context for every row */
   int32_t partition_tokens;    /* split-K partition (multiple of 32); 0 = library choice: for
-                                  GQA groups >= 4 and block_size >= 32 (16 at head_dim 256) a
-                                  balanced split of all key tiles over one resident grid,
-                                  otherwise a partition sized from the batch */
+                                  GQA groups >= 4 and block_size >= 64 / (head_dim / 8) (4 at
+                                  head_dim 128, 8 at 64, 2 at 256) a balanced split of all
+                                  key tiles over one resident grid, otherwise a partition
+                                  sized from the batch */
   void* out;                   /* bf16 [rows, out_row_stride] */
   int64_t out_row_stride;      /* elements */
   /* Optional fused KV store of the new token rows (NULL new_key = none): written
@@ -122,7 +123,8 @@ int gk_paged_decode(const gk_decode_params* params, void* workspace, size_t work
  * [left, seq_prefix[s] + i] of block-table row seq_request[s] (causal; left =
  * position - sliding_window + 1 when a window is set, else 0). Every key,
  * including the chunk's own, must already be in the pool (store first).
- * head_dim 64 or 128; GQA group at most 128; block_size a power of two >= 32.
+ * head_dim 64 or 128; GQA group at most 128; block_size a power of two of at
+ * least 64 / (head_dim / 8) keys (4 at head_dim 128, 8 at 64).
  * ------------------------------------------------------------------------- */
 typedef struct gk_prefill_params {
   size_t struct_size;          /* sizeof(gk_prefill_params) as the caller was built; checked */

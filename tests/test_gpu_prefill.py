@@ -52,10 +52,41 @@ def test_prefill_geometries(runner, geometry):
     print("geometry", geometry, check(case, runner.run_prefill_case(case)), flush=True)
 
 
-@pytest.mark.parametrize("block_size", [32, 128, 256])
+@pytest.mark.parametrize("block_size", [4, 8, 16, 32, 128, 256])
 def test_prefill_block_sizes(runner, block_size):
+    # Blocks shorter than a 32-key step: every load instruction of a step (4
+    # keys at d 128) reads its own block-table entry.
     case = cases.PrefillCase(block_size, 32, 8, 128, block_size, prefixes=[5, 600, 0], chunks=[300, 31, 129])
     check(case, runner.run_prefill_case(case))
+
+
+@pytest.mark.parametrize("block_size", [8, 16])
+def test_prefill_small_blocks_head_dim_64(runner, block_size):
+    case = cases.PrefillCase(50 + block_size, 14, 2, 64, block_size, prefixes=[3, 257], chunks=[140, 66])
+    check(case, runner.run_prefill_case(case))
+
+
+@pytest.mark.parametrize("block_size", [4, 16])
+def test_prefill_small_blocks_window_evicted(runner, block_size):
+    # Sliding window over short blocks: every slot no row sees is poisoned
+    # (NaN) and the table entries of blocks wholly before every row's window
+    # are -1, as after eviction. Runs of a step outside a workgroup's keys read
+    # the nearest owned block, and their V rows are zeroed.
+    import copy
+
+    case = cases.PrefillCase(60 + block_size, 16, 4, 128, block_size, prefixes=[100, 0, 333, 64], chunks=[90, 200, 17, 1],
+                             window=70)
+    used = np.zeros(case.slots, dtype=bool)
+    evicted = case.block_tables.copy()
+    for s, (prefix, chunk) in enumerate(zip(case.prefixes, case.chunks)):
+        first = max(0, int(prefix) - case.window + 1)
+        for t in range(first, int(prefix + chunk)):
+            used[case.block_tables[s, t // block_size] * block_size + t % block_size] = True
+        evicted[s, :first // block_size] = -1
+    case.pool[:, :, ~used, :] = 0x7fc0
+    reference = copy.copy(case)
+    case.block_tables = evicted
+    check(reference, runner.run_prefill_case(case), fp32_softmax=True)
 
 
 def test_prefill_shared_prefix_small(runner):
@@ -83,11 +114,13 @@ def test_prefill_poisoned_unused_slots(runner):
 
 
 def test_prefill_rejects_small_blocks(runner):
+    # Blocks shorter than one load instruction's keys (4 at d 128, 8 at d 64).
     from gaudirt_amd import capi
     import torch
-    p = capi.PrefillParams()
-    p.head_dim, p.q_heads, p.kv_heads, p.block_size, p.slots, p.scale = 128, 8, 2, 16, 1024, 0.1
-    assert capi.load().gk_paged_prefill(ctypes.byref(p), None) == capi.GK_ERR_UNSUPPORTED
+    for d, block in [(128, 2), (64, 4), (128, 1)]:
+        p = capi.PrefillParams()
+        p.head_dim, p.q_heads, p.kv_heads, p.block_size, p.slots, p.scale = d, 8, 2, block, 1024, 0.1
+        assert capi.load().gk_paged_prefill(ctypes.byref(p), None) == capi.GK_ERR_UNSUPPORTED, (d, block)
     del torch
 
 

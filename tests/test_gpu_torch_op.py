@@ -212,7 +212,8 @@ def test_kv_pool_allocation_and_reuse(torch_ext):
         gaudirt_amd.allocate_paged_kv(1, 100, 2, 96)
 
 
-@pytest.mark.parametrize("heads,kv_heads,dim,block", [(32, 8, 128, 64), (8, 2, 64, 128), (16, 16, 128, 32)])
+@pytest.mark.parametrize("heads,kv_heads,dim,block", [(32, 8, 128, 64), (8, 2, 64, 128), (16, 16, 128, 32),
+                                                      (32, 8, 128, 16), (16, 4, 128, 4), (8, 2, 64, 8)])
 def test_mixed_prefill_and_decode_batch(torch_ext, heads, kv_heads, dim, block):
     """A batch mixing chunked-prefill runs (>= 8 consecutive positions: MFMA
     prefill kernel) and single decode rows (decode kernel via row_map), with a
