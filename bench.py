@@ -60,11 +60,11 @@ def parse_args():
     return ap.parse_args()
 
 
-def measured_traffic(workload):
-    """HBM bytes per launch of the decode kernel, as last measured with rocprofv3 PMC
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of the dominant kernel, as last measured with rocprofv3 PMC
     (FETCH_SIZE x2 + WRITE_SIZE) and recorded with its command in
-    profiles/decode_stream_<workload>_traffic.md; None when no measurement exists."""
-    path = os.path.join(ROOT, "profiles", f"decode_stream_{workload}_traffic.md")
+    profiles/<kernel>_<workload>_traffic.md; None when no measurement exists."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.md")
     try:
         with open(path) as fh:
             for line in fh:
@@ -153,7 +153,7 @@ def prefill_bench(args):
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic", "config": {"workload": f"c4: {WORKLOADS['c4']}", "flops_per_step": pc.flops()},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None},
+                     "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": measured_traffic("prefill", "c4")},
         "cpu_baseline": None}), flush=True)
 
 
@@ -269,7 +269,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": measured_traffic(args.workload),
+            "traffic": measured_traffic("decode_stream", args.workload),
         },
         "cpu_baseline": cpu,
     }
