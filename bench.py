@@ -110,8 +110,22 @@ def cpu_baseline(dc, target_seconds):
         "cores": threads,
         "kind": "port",
         "sample": f"first {rows} of {dc.batch} sequences ({kv_tokens} KV tokens), direct_bf16_pv C oracle, "
-                  f"median of {reps} run(s), {t:.3f} s each",
+                  f"median of {reps} run(s), {t:.3f} s each, {threads} threads on {host_cpu()}",
     }
+
+
+def host_cpu():
+    """CPU model and logical CPU count of the host, for the baseline's record."""
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{model} ({os.cpu_count()} logical CPUs visible)"
 
 
 def prefill_bench(args):

@@ -417,7 +417,7 @@ def test_fused_scheduler_metadata(torch_ext):
         assert torch.equal(metadata.model_positions().cpu(), positions)
 
 
-@pytest.mark.parametrize("page", [32, 128])
+@pytest.mark.parametrize("page", [4, 16, 32, 128])
 def test_page_aligned_device_metadata(torch_ext, page):
     """Device-detected pages: block tables built on the device, prefill runs
     whose requests are gathered on the device; output equal to the host
