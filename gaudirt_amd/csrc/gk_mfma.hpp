@@ -74,6 +74,13 @@ __device__ __forceinline__ float col4_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// s_waitcnt vmcnt(0) that LLVM's wait-count tracking sees (encoding: vmcnt 0,
+// expcnt and lgkmcnt at their maxima). Afterwards it treats every earlier
+// vector load as complete, so it inserts no wait of its own before their
+// registers are read: its model does not count the asm direct loads, and a
+// wait it placed after some of them would also wait for those.
+__device__ __forceinline__ void wait_vmem_visible() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 // Wait until at most N vector memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmem() {

@@ -77,14 +77,22 @@ struct PrefillShape {
   static constexpr int NI = TILE / 1024;            // 1 KiB load instructions per tile
 };
 
-// SMALL: pool blocks shorter than a step's 32 keys (but at least one load's
-// 64 / (D / 8) keys); each load of a step then reads its own block-table entry.
-template <int D, bool SOFTCAP, bool SMALL>
+// How a step's slots are found (the MODE template argument):
+//  kStepBlocks  blocks of >= 32 keys: one scalar block-table entry per step;
+//  kLoadBlocks  blocks of >= 64 / (D / 8) keys (one load instruction's): one
+//               scalar entry per load instruction;
+//  kKeyBlocks   shorter blocks, down to the token-granular map (block 1): each
+//               lane reads its own key's entry with a vector load.
+constexpr int kStepBlocks = 0, kLoadBlocks = 1, kKeyBlocks = 2;
+
+template <int D, bool SOFTCAP, int MODE>
 __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_kernel(PrefillArgs a) {
   using S = PrefillShape<D>;
-  constexpr int LPW = S::NI / kPrefillWaves;  // load instructions per wave per K (or V) tile
-  constexpr int NE = SMALL ? LPW : 1;         // block-table entries per wave per step
-  constexpr int KPL = kKeys / S::NI;          // keys of one load instruction
+  constexpr int LPW = S::NI / kPrefillWaves;         // load instructions per wave per K (or V) tile
+  constexpr int NE = MODE == kStepBlocks ? 1 : LPW;  // block-table entries per wave (per lane) per step
+  constexpr int KPL = kKeys / S::NI;                 // keys of one load instruction
+  constexpr bool CLAMPED = MODE != kStepBlocks;      // entries of keys outside [key_begin, key_end) clamped
+  static_assert(MODE != kKeyBlocks || kStages == 2, "per-lane entries rely on the step's full drain");
   // kStages K/V stages. The direct loads are asm statements the compiler does
   // not track, so one array serves every stage; reads are ordered by the
   // explicit vmcnt wait and the barrier of each step.
@@ -157,9 +165,9 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
 
   // Direct loads of the 32-key step at tb into one stage. Steps are 32-aligned.
   // Blocks of >= 32 keys hold a whole step: its slots are consecutive from the
-  // block's slot for tb (one scalar block-table read). Shorter blocks (SMALL)
-  // hold whole load instructions (KPL keys each): each of this wave's loads
-  // reads its own entry.
+  // block's slot for tb (one scalar block-table read). Blocks of >= KPL keys
+  // hold whole load instructions: each of this wave's loads reads its own
+  // entry. Shorter blocks: each lane reads the entry of its own key.
   // Piece p = 64 ins + lane of load instruction ins (wave ins % waves): token
   // p / CPR, stored chunk p % CPR holding the token's chunk (p % CPR) ^
   // swz(token, D / 8).
@@ -167,42 +175,55 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
     int e[NE];
   };
   auto issue = [&](int tb, const Entries& en, char* kt, char* vt) {
+    // Per-lane entries are vector loads of the previous step, already complete
+    // (the loop waits for every load before its barrier); say so to the compiler.
+    if constexpr (MODE == kKeyBlocks) wait_vmem_visible();
     const uint32_t kl = lds_addr(kt), vl = lds_addr(vt);
 #pragma unroll
     for (int k = 0; k < LPW; ++k) {
       const int ins = wave + k * kPrefillWaves;
       const int p = ins * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
-      const int run = SMALL ? ins * KPL : 0;  // first key of the entry's run, relative to tb
-      const uint32_t row0 = (uint32_t)((en.e[SMALL ? k : 0] << shift) | ((tb + run) & bmask)) * (2 * D);
-      const uint32_t off = row0 + (tt - run) * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4);
+      uint32_t row;  // byte offset of the lane's key row
+      if constexpr (MODE == kKeyBlocks) {
+        row = (uint32_t)((en.e[k] << shift) | ((tb + tt) & bmask)) * (2 * D);
+      } else {
+        const int run = MODE == kLoadBlocks ? ins * KPL : 0;  // first key of the entry's run, relative to tb
+        row = (uint32_t)((en.e[MODE == kLoadBlocks ? k : 0] << shift) | ((tb + run) & bmask)) * (2 * D) +
+              (tt - run) * (2 * D);
+      }
+      const uint32_t off = row + ((pc ^ swz(tt, D / 8)) << 4);
       lds_dma16(kl + ins * 1024, krs, off);
       lds_dma16(vl + ins * 1024, vrs, off);
     }
   };
-  // Block-table entries of the step at key tb (scalar loads, fetched a step
-  // ahead). A run wholly outside the keys [key_begin, key_end) takes the
-  // entry of the nearest such key, so that only blocks the request owns are
-  // read; its keys are masked (and their V rows zeroed).
+  // Block-table entries of the step at key tb (scalar loads, or per-lane
+  // vector loads for kKeyBlocks, fetched a step ahead: the loop's wait before
+  // the barrier covers them). With CLAMPED a key outside [key_begin, key_end)
+  // takes the entry of the nearest such key, so that only blocks the request
+  // owns are read; its keys are masked (and their V rows zeroed).
   auto entry_of = [&](int tb) {
     Entries en;
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
-      int key = tb + (SMALL ? (wave + k * kPrefillWaves) * KPL : 0);
-      if constexpr (SMALL) key = min(max(key, key_begin), key_end - 1);
-      en.e[k] = scalar_load(bt, key >> shift);
+      int key = tb;
+      if constexpr (MODE == kLoadBlocks) key += (wave + k * kPrefillWaves) * KPL;
+      if constexpr (MODE == kKeyBlocks) key += (wave + k * kPrefillWaves) * KPL + lane / S::CPR;
+      if constexpr (CLAMPED) key = min(max(key, key_begin), key_end - 1);
+      if constexpr (MODE == kKeyBlocks) en.e[k] = bt[key >> shift];
+      else en.e[k] = scalar_load(bt, key >> shift);
     }
     return en;
   };
 
   auto consume = [&](int tb, const char* kt, char* vt) {
-    if (tb + kKeys > key_end || (SMALL && tb < key_begin)) {
+    if (tb + kKeys > key_end || (CLAMPED && tb < key_begin)) {
       // Keys past the tile's last row (and, with short blocks, keys before the
       // window's first, read from the nearest owned block) hold arbitrary pool
       // data: zero their V rows so that a zero probability cannot meet a
       // non-finite value. Whole-block keys before the window are stored tokens.
       for (int p = tid; p < kKeys * S::CPR; p += kPrefillWaves * 64) {
         const int key = tb + p / S::CPR;
-        if (key >= key_end || (SMALL && key < key_begin))
+        if (key >= key_end || (CLAMPED && key < key_begin))
           *reinterpret_cast<uint4*>(vt + p * 16) = make_uint4(0, 0, 0, 0);
       }
       __syncthreads();
@@ -329,6 +350,10 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
     else if (later == 1) wait_vmem<LPS>();
     else wait_vmem<0>();
     __syncthreads();
+    // Every load of this wave has landed; with per-lane entries (the only
+    // compiler-visible loads in the loop) tell the compiler, so that it adds no
+    // wait of its own after this step's direct loads.
+    if constexpr (MODE == kKeyBlocks) wait_vmem_visible();
     const int ahead = step + kStages - 1;
     if (ahead < nsteps) {
       const int buf = ahead % kStages;
@@ -356,15 +381,17 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   }
 }
 
+template <int D, int MODE>
+void launch_mode(const PrefillArgs& a, bool softcap, dim3 grid, hipStream_t stream) {
+  if (softcap) prefill_kernel<D, true, MODE><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+  else prefill_kernel<D, false, MODE><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+}
+
 template <int D>
-void launch(const PrefillArgs& a, bool softcap, bool small, dim3 grid, hipStream_t stream) {
-  if (small) {
-    if (softcap) prefill_kernel<D, true, true><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
-    else prefill_kernel<D, false, true><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
-  } else {
-    if (softcap) prefill_kernel<D, true, false><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
-    else prefill_kernel<D, false, false><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
-  }
+void launch(const PrefillArgs& a, bool softcap, int block_size, dim3 grid, hipStream_t stream) {
+  if (block_size >= kKeys) launch_mode<D, kStepBlocks>(a, softcap, grid, stream);
+  else if (block_size >= kKeys / PrefillShape<D>::NI) launch_mode<D, kLoadBlocks>(a, softcap, grid, stream);
+  else launch_mode<D, kKeyBlocks>(a, softcap, grid, stream);
 }
 
 }  // namespace
@@ -377,11 +404,8 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
     return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: head dimension must be 64 or 128");
   if (p->q_heads <= 0 || p->kv_heads <= 0 || p->q_heads % p->kv_heads || p->q_heads / p->kv_heads > kQrows)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: invalid head geometry (GQA group at most 128)");
-  // One load instruction covers 64 / (head_dim / 8) keys: 4 at 128, 8 at 64.
-  const int min_block = 64 / (p->head_dim / 8);
-  if (!is_pow2(p->block_size) || p->block_size < min_block || p->block_size > (1 << 20))
-    return fail(GK_ERR_UNSUPPORTED,
-                "gk_paged_prefill: block_size must be a power of two of at least 4 (head_dim 128) or 8 (64)");
+  if (!is_pow2(p->block_size) || p->block_size > (1 << 20))
+    return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: block_size must be a power of two of at most 2^20");
   if (p->seqs < 0 || p->seqs > 65535 || p->max_rows < 0 || p->slots <= 0)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: sequence count, rows or slots out of range");
   if (p->slots > (int64_t)(UINT32_MAX / 2) / p->head_dim)
@@ -423,9 +447,8 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
   const int64_t items = (int64_t)a.tiles * p->kv_heads * p->seqs;
   if (items > (int64_t)1 << 30) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: too many rows");
   const dim3 grid((unsigned)items);
-  const bool small = p->block_size < kKeys;
-  if (p->head_dim == 64) launch<64>(a, softcap, small, grid, stream);
-  else launch<128>(a, softcap, small, grid, stream);
+  if (p->head_dim == 64) launch<64>(a, softcap, p->block_size, grid, stream);
+  else launch<128>(a, softcap, p->block_size, grid, stream);
   return hip_status(hipGetLastError(), "gk_paged_prefill launch");
 }
 

@@ -123,8 +123,8 @@ int gk_paged_decode(const gk_decode_params* params, void* workspace, size_t work
  * [left, seq_prefix[s] + i] of block-table row seq_request[s] (causal; left =
  * position - sliding_window + 1 when a window is set, else 0). Every key,
  * including the chunk's own, must already be in the pool (store first).
- * head_dim 64 or 128; GQA group at most 128; block_size a power of two of at
- * least 64 / (head_dim / 8) keys (4 at head_dim 128, 8 at 64).
+ * head_dim 64 or 128; GQA group at most 128; block_size any power of two up
+ * to 2^20, 1 (the token-granular slot map as the block table) included.
  * ------------------------------------------------------------------------- */
 typedef struct gk_prefill_params {
   size_t struct_size;          /* sizeof(gk_prefill_params) as the caller was built; checked */

@@ -52,21 +52,22 @@ def test_prefill_geometries(runner, geometry):
     print("geometry", geometry, check(case, runner.run_prefill_case(case)), flush=True)
 
 
-@pytest.mark.parametrize("block_size", [4, 8, 16, 32, 128, 256])
+@pytest.mark.parametrize("block_size", [1, 2, 4, 8, 16, 32, 128, 256])
 def test_prefill_block_sizes(runner, block_size):
     # Blocks shorter than a 32-key step: every load instruction of a step (4
-    # keys at d 128) reads its own block-table entry.
+    # keys at d 128) reads its own block-table entry; below 4 keys (down to the
+    # token-granular map) every lane reads its own key's entry.
     case = cases.PrefillCase(block_size, 32, 8, 128, block_size, prefixes=[5, 600, 0], chunks=[300, 31, 129])
     check(case, runner.run_prefill_case(case))
 
 
-@pytest.mark.parametrize("block_size", [8, 16])
+@pytest.mark.parametrize("block_size", [1, 4, 8, 16])
 def test_prefill_small_blocks_head_dim_64(runner, block_size):
     case = cases.PrefillCase(50 + block_size, 14, 2, 64, block_size, prefixes=[3, 257], chunks=[140, 66])
     check(case, runner.run_prefill_case(case))
 
 
-@pytest.mark.parametrize("block_size", [4, 16])
+@pytest.mark.parametrize("block_size", [1, 2, 4, 16])
 def test_prefill_small_blocks_window_evicted(runner, block_size):
     # Sliding window over short blocks: every slot no row sees is poisoned
     # (NaN) and the table entries of blocks wholly before every row's window
@@ -113,11 +114,10 @@ def test_prefill_poisoned_unused_slots(runner):
     check(case, runner.run_prefill_case(case))
 
 
-def test_prefill_rejects_small_blocks(runner):
-    # Blocks shorter than one load instruction's keys (4 at d 128, 8 at d 64).
+def test_prefill_rejects_bad_blocks(runner):
     from gaudirt_amd import capi
     import torch
-    for d, block in [(128, 2), (64, 4), (128, 1)]:
+    for d, block in [(128, 3), (64, 24), (128, 1 << 21), (128, 0)]:
         p = capi.PrefillParams()
         p.head_dim, p.q_heads, p.kv_heads, p.block_size, p.slots, p.scale = d, 8, 2, block, 1024, 0.1
         assert capi.load().gk_paged_prefill(ctypes.byref(p), None) == capi.GK_ERR_UNSUPPORTED, (d, block)

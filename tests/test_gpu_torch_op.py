@@ -213,7 +213,8 @@ def test_kv_pool_allocation_and_reuse(torch_ext):
 
 
 @pytest.mark.parametrize("heads,kv_heads,dim,block", [(32, 8, 128, 64), (8, 2, 64, 128), (16, 16, 128, 32),
-                                                      (32, 8, 128, 16), (16, 4, 128, 4), (8, 2, 64, 8)])
+                                                      (32, 8, 128, 16), (16, 4, 128, 4), (8, 2, 64, 8),
+                                                      (32, 8, 128, 1), (8, 2, 64, 2)])
 def test_mixed_prefill_and_decode_batch(torch_ext, heads, kv_heads, dim, block):
     """A batch mixing chunked-prefill runs (>= 8 consecutive positions: MFMA
     prefill kernel) and single decode rows (decode kernel via row_map), with a
