@@ -47,9 +47,8 @@ struct MfmaShape {
 };
 
 // Balanced ("stream") decode schedule, head dims 64/128/256, GQA group >= 4,
-// block_size >= 64 / MfmaShape<D>::CPR (the keys of one 16-byte load per lane).
-// Workspace layout: part_o[2 * wgs][hpw][D], part_ml[2 * wgs][hpw][2] and
-// unit_span[units] (int32 pairs).
+// any block size. Workspace layout: part_o[2 * wgs][hpw][D],
+// part_ml[2 * wgs][hpw][2] and unit_span[units] (int32 pairs).
 int stream_decode_wgs(int head_dim, bool softcap, int block_size);
 size_t stream_decode_workspace_bytes(int head_dim, int heads_per_group, int64_t units, int wgs);
 int launch_stream_decode(const DecodeArgs& a, bool softcap, int head_dim, int wgs, void* workspace,

@@ -19,8 +19,10 @@
 //
 // Tiles are TS-key ranges at absolute key positions (tile k = keys [k TS,
 // (k + 1) TS)), so with block_size >= TS every tile lies in one pool block and
-// needs one block-table entry, fetched with a scalar load one tile ahead. Keys
-// outside a row's visible range [left, ctx) are masked. Inside a unit the
+// needs one block-table entry, fetched with a scalar load one tile ahead;
+// shorter blocks take one entry per 16-byte load or, below one load's keys,
+// one per key (the MODE template argument). Keys outside a row's visible
+// range [left, ctx) are masked. Inside a unit the
 // tiles are visited rotated by kv_head * count / kv_heads: the kv heads of a
 // row then stream different blocks at any moment, instead of the same block
 // offset in regions a power-of-two apart, which concentrates the reads on a
@@ -109,17 +111,28 @@ struct TileDesc {
 template <int NR>
 struct TileEntries {
   int e[NR];
+  int keyed;  // per-key entries packed into one VGPR, lane k = key k (kKeyBlocks)
 };
 
-// SMALL: pool blocks shorter than a tile (but at least one load's TS / LOADS
-// keys); each load of a tile then reads its own block-table entry.
-template <int D, bool SOFTCAP, bool SMALL>
+// How a tile's slots are found (the MODE template argument):
+//  kTileBlocks  blocks of >= TS keys: one block-table entry per tile;
+//  kLoadBlocks  blocks of >= 64 / CPR keys (one 16-byte load per lane): one
+//               entry per load instruction;
+//  kKeyBlocks   shorter blocks, down to the token-granular map (block 1): one
+//               entry per key, each lane picking its key's among the load's.
+// All entries are scalar loads issued one tile ahead.
+constexpr int kTileBlocks = 0, kLoadBlocks = 1, kKeyBlocks = 2;
+
+template <int D, bool SOFTCAP, int MODE>
 __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   using S = MfmaShape<D>;
   constexpr int TS = S::TS;
-  constexpr int NR = SMALL ? S::LOADS : 1;  // key runs of a tile
-  constexpr int KPR = TS / NR;              // keys of one run
-  using TileDesc = gk::TileDesc<NR>;
+  constexpr int NR = MODE == kTileBlocks ? 1 : MODE == kLoadBlocks ? S::LOADS : TS;  // key runs of a tile
+  constexpr int KPR = TS / NR;  // keys of one run
+  constexpr int KPL = 64 / S::CPR;  // keys of one load instruction
+  // kKeyBlocks hands its per-key entries straight from the prefetch to the
+  // loads (a descriptor holding TS offsets would live in scratch memory).
+  using TileDesc = gk::TileDesc<MODE == kKeyBlocks ? 1 : NR>;
   constexpr int QBYTES = 16 * D * 2;  // one unit's query heads (up to 16)
   // Two K/V stages, each tile its own LDS object so that the compiler tells
   // reads of one from the direct loads in flight into another, and the two
@@ -246,15 +259,25 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     TileEntries<NR> r;
     const int tb = tile_key(c);
     const int64_t bt_row = (int64_t)c.req * a.bt_stride;
+    if constexpr (MODE == kKeyBlocks) {
+      if (shift == 0 && tb >= c.rt.left && tb + TS <= c.rt.ctx) {
+        // Token-granular map, every key of the tile visible: TS consecutive
+        // entries, all in range (wide scalar loads).
+#pragma unroll
+        for (int i = 0; i < NR; ++i) r.e[i] = scalar_load(a.block_tables, bt_row + tb + i);
+        return r;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       int key = tb + i * KPR;
-      if constexpr (SMALL) key = min(max(key, c.rt.left), c.rt.ctx - 1);
+      if constexpr (MODE != kTileBlocks) key = min(max(key, c.rt.left), c.rt.ctx - 1);
       r.e[i] = c.rt.ctx > 0 ? scalar_load(a.block_tables, bt_row + (key >> shift)) : 0;
     }
     return r;
   };
   auto describe = [&](const Cursor& c, const TileEntries<NR>& en) {
+    constexpr int NROW = MODE == kKeyBlocks ? 1 : NR;
     TileDesc t;
     t.tb = tile_key(c);
     t.left = c.rt.left;
@@ -267,7 +290,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     t.qrow = c.qrow;
     t.g = c.g;
 #pragma unroll
-    for (int i = 0; i < NR; ++i)
+    for (int i = 0; i < NROW; ++i)
       t.row0[i] = (((uint32_t)en.e[i] << shift) | (uint32_t)((t.tb + i * KPR) & block_mask)) * (uint32_t)(2 * D);
     t.q_start = c.j == 0 || c.g == g_begin;
     t.q_end = c.j == c.rt.count - 1 || c.g == g_end - 1;
@@ -278,7 +301,27 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   const uint32_t region = (uint32_t)(a.slots * D * 2);
   // K and V tiles -> LDS: load i, lane l fills piece s = 64 i + l, i.e. key
   // s / CPR, stored chunk s % CPR, which holds the key's chunk (s % CPR) ^ swz.
-  auto issue_tile = [&](const TileDesc& t, char* kt, char* vt) {
+  // Byte offset of the row of key tt of the tile (this lane's key of load i).
+  // kKeyBlocks: lane k of `keyed` holds key k's entry (written lane by lane
+  // from the scalar entries); each lane fetches its own key's with a permute.
+  auto row_of = [&](const TileDesc& t, int keyed, int i, int tt) -> uint32_t {
+    if constexpr (MODE == kTileBlocks) return t.row0[0] + tt * (2 * D);
+    if constexpr (MODE == kLoadBlocks) return t.row0[i] + (tt - i * KPR) * (2 * D);
+    const int e = __builtin_amdgcn_ds_bpermute(tt << 2, keyed);
+    return (((uint32_t)e << shift) | (uint32_t)((t.tb + tt) & block_mask)) * (uint32_t)(2 * D);
+  };
+  // kKeyBlocks: pack the prefetched scalar entries into one VGPR (lane k =
+  // key k), so that one register instead of TS carries them to the loads.
+  auto pack = [&](TileEntries<NR>& en) {
+    if constexpr (MODE == kKeyBlocks) {
+      int keyed = 0;
+#pragma unroll
+      for (int k = 0; k < TS; ++k) asm("v_writelane_b32 %0, %1, %2" : "=v"(keyed) : "s"(en.e[k]), "i"(k), "0"(keyed));
+      en.keyed = keyed;
+    }
+  };
+  auto issue_tile = [&](const TileDesc& t, const TileEntries<NR>& en, char* kt, char* vt) {
+    const int keyed = en.keyed;
     const uint16_t* kbase = a.pool + (int64_t)t.kvh * a.slots * D;
     const uint16_t* vbase = kbase + (int64_t)a.kv_heads * a.slots * D;
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, region, kBufferDword3);
@@ -287,14 +330,12 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
-      const uint32_t row = SMALL ? t.row0[i] + (tt - i * KPR) * (2 * D) : t.row0[0] + tt * (2 * D);
-      lds_dma16(kl + i * 1024, krs, row + ((pc ^ swz(tt, D / 8)) << 4));
+      lds_dma16(kl + i * 1024, krs, row_of(t, keyed, i, tt) + ((pc ^ swz(tt, D / 8)) << 4));
     }
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
-      const uint32_t row = SMALL ? t.row0[i] + (tt - i * KPR) * (2 * D) : t.row0[0] + tt * (2 * D);
-      lds_dma16(vl + i * 1024, vrs, row + ((pc ^ swz(tt, D / 8)) << 4));
+      lds_dma16(vl + i * 1024, vrs, row_of(t, keyed, i, tt) + ((pc ^ swz(tt, D / 8)) << 4));
     }
   };
   // The unit's query heads -> LDS ([head][D], row-major). The resource covers
@@ -538,15 +579,18 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   // Stage 0 / stage 1 alternate; the query buffer alternates per unit.
   int64_t to_issue = g_end - g_begin;  // tiles not yet issued
   int qpar = 0;
-  TileDesc d0 = describe(cur, table_entry(cur)), d1;
+  TileEntries<NR> first_entry = table_entry(cur);
+  pack(first_entry);
+  TileDesc d0 = describe(cur, first_entry), d1;
   int qp0 = 0, qp1 = 0;                // query buffer of the tile in stage 0 / 1
   if (d0.q_start) issue_query(d0, qs[0]);
-  issue_tile(d0, kt0, vt0);
+  issue_tile(d0, first_entry, kt0, vt0);
   --to_issue;
   TileEntries<NR> next_entry = {};
   if (to_issue > 0) {
     advance(cur);
     next_entry = table_entry(cur);
+    pack(next_entry);
   }
   while (true) {
     bool more = to_issue > 0;
@@ -557,12 +601,13 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
         issue_query(d1, qs[qpar]);
       }
       qp1 = qpar;
-      issue_tile(d1, kt1, vt1);
+      issue_tile(d1, next_entry, kt1, vt1);
       if (--to_issue > 0) {
         advance(cur);
         next_entry = table_entry(cur);
       }
       wait_vmem<2 * S::LOADS>();
+      pack(next_entry);  // its scalar loads landed during the wait
     } else {
       wait_vmem<0>();
     }
@@ -577,12 +622,13 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
         issue_query(d0, qs[qpar]);
       }
       qp0 = qpar;
-      issue_tile(d0, kt0, vt0);
+      issue_tile(d0, next_entry, kt0, vt0);
       if (--to_issue > 0) {
         advance(cur);
         next_entry = table_entry(cur);
       }
       wait_vmem<2 * S::LOADS>();
+      pack(next_entry);  // its scalar loads landed during the wait
     } else {
       wait_vmem<0>();
     }
@@ -660,24 +706,46 @@ __global__ __launch_bounds__(64) void stream_merge_kernel(StreamMergeArgs m) {
   for (int e = 0; e < PER_LANE; ++e) dst[lane + 64 * e] = (uint16_t)bf16_bits(acc[e] * inv);
 }
 
-template <int D, bool SOFTCAP, bool SMALL>
+template <int D, bool SOFTCAP, int MODE>
 int resident_per_cu() {
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<D, SOFTCAP, SMALL>, 64, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_stream_kernel<D, SOFTCAP, MODE>, 64, 0) !=
           hipSuccess ||
       n <= 0)
     n = 1;
   return n;
 }
 
-template <int D>
-int resident_per_cu(bool softcap, bool small) {
-  if (small) return softcap ? resident_per_cu<D, true, true>() : resident_per_cu<D, false, true>();
-  return softcap ? resident_per_cu<D, true, false>() : resident_per_cu<D, false, false>();
+template <int D, int MODE>
+int resident_per_cu(bool softcap) {
+  return softcap ? resident_per_cu<D, true, MODE>() : resident_per_cu<D, false, MODE>();
 }
 
-// Blocks shorter than a tile take the per-load block-table variant.
-bool small_blocks(int head_dim, int block_size) { return block_size < (head_dim == 256 ? 16 : 32); }
+template <int D>
+int resident_per_cu(bool softcap, int mode) {
+  if (mode == kKeyBlocks) return resident_per_cu<D, kKeyBlocks>(softcap);
+  if (mode == kLoadBlocks) return resident_per_cu<D, kLoadBlocks>(softcap);
+  return resident_per_cu<D, kTileBlocks>(softcap);
+}
+
+template <int D, int MODE>
+void launch_stream_mode(const StreamArgs& sa, bool softcap, dim3 grid, hipStream_t stream) {
+  if (softcap) decode_stream_kernel<D, true, MODE><<<grid, 64, 0, stream>>>(sa);
+  else decode_stream_kernel<D, false, MODE><<<grid, 64, 0, stream>>>(sa);
+}
+
+template <int D>
+void launch_stream_kernel(const StreamArgs& sa, bool softcap, int mode, dim3 grid, hipStream_t stream) {
+  if (mode == kKeyBlocks) launch_stream_mode<D, kKeyBlocks>(sa, softcap, grid, stream);
+  else if (mode == kLoadBlocks) launch_stream_mode<D, kLoadBlocks>(sa, softcap, grid, stream);
+  else launch_stream_mode<D, kTileBlocks>(sa, softcap, grid, stream);
+}
+
+// Slot lookup of a block size (the kernel's MODE).
+int block_mode(int head_dim, int block_size) {
+  const int ts = head_dim == 256 ? 16 : 32, keys_per_load = 64 / (head_dim / 8);
+  return block_size >= ts ? kTileBlocks : block_size >= keys_per_load ? kLoadBlocks : kKeyBlocks;
+}
 
 }  // namespace
 
@@ -687,19 +755,19 @@ int device_cus();
 // resident (LDS-bound), queried once per device and kernel variant.
 int stream_decode_wgs(int head_dim, bool softcap, int block_size) {
   static std::mutex mu;
-  static int cached[64][3][2][2] = {};
+  static int cached[64][3][2][3] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   const int di = head_dim == 64 ? 0 : (head_dim == 128 ? 1 : 2);
-  const bool small = small_blocks(head_dim, block_size);
+  const int mode = block_mode(head_dim, block_size);
   std::lock_guard<std::mutex> lock(mu);
-  int& slot = cached[dev][di][softcap ? 1 : 0][small ? 1 : 0];
+  int& slot = cached[dev][di][softcap ? 1 : 0][mode];
   if (!slot) {
     int per_cu = 1;
     switch (head_dim) {
-      case 64: per_cu = resident_per_cu<64>(softcap, small); break;
-      case 128: per_cu = resident_per_cu<128>(softcap, small); break;
-      default: per_cu = resident_per_cu<256>(softcap, small); break;
+      case 64: per_cu = resident_per_cu<64>(softcap, mode); break;
+      case 128: per_cu = resident_per_cu<128>(softcap, mode); break;
+      default: per_cu = resident_per_cu<256>(softcap, mode); break;
     }
     slot = device_cus() * per_cu;
   }
@@ -727,21 +795,12 @@ int launch_stream_decode(const DecodeArgs& a, bool softcap, int head_dim, int wg
   sa.unit_span = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes + ml_bytes);
 
   const dim3 grid(wgs);
-  const bool small = small_blocks(head_dim, 1 << a.block_shift);
-#define GK_STREAM_LAUNCH(D)                                                                      \
-  if (small) {                                                                                   \
-    if (softcap) decode_stream_kernel<D, true, true><<<grid, 64, 0, stream>>>(sa);               \
-    else decode_stream_kernel<D, false, true><<<grid, 64, 0, stream>>>(sa);                      \
-  } else {                                                                                       \
-    if (softcap) decode_stream_kernel<D, true, false><<<grid, 64, 0, stream>>>(sa);              \
-    else decode_stream_kernel<D, false, false><<<grid, 64, 0, stream>>>(sa);                     \
-  }
+  const int mode = block_mode(head_dim, 1 << a.block_shift);
   switch (head_dim) {
-    case 64: GK_STREAM_LAUNCH(64) break;
-    case 128: GK_STREAM_LAUNCH(128) break;
-    default: GK_STREAM_LAUNCH(256) break;
+    case 64: launch_stream_kernel<64>(sa, softcap, mode, grid, stream); break;
+    case 128: launch_stream_kernel<128>(sa, softcap, mode, grid, stream); break;
+    default: launch_stream_kernel<256>(sa, softcap, mode, grid, stream); break;
   }
-#undef GK_STREAM_LAUNCH
   if (int rc = hip_status(hipGetLastError(), "gk_paged_decode stream launch")) return rc;
 
   StreamMergeArgs m{};

@@ -722,14 +722,12 @@ int device_cus() {
 //  - Otherwise 2048-key items while one round of them (at the expected mean
 //    length max_context / 2) fits the resident waves, else 1024.
 // dot2 path: halve a 2048-key partition until the items fill the GPU.
-// The balanced schedule (decode_stream.hip) serves the MFMA path whenever the
-// caller leaves the partition to the library and the keys one 16-byte load
-// per lane covers (64 / (head_dim / 8)) lie in one pool block; an explicit
-// partition, smaller blocks and small groups take the partitioned kernels.
+// The balanced schedule (decode_stream.hip) serves the MFMA path, every block
+// size included, whenever the caller leaves the partition to the library; an
+// explicit partition and small groups take the partitioned kernels.
 bool use_stream(const gk_decode_params* p) {
   const int group = p->q_heads / p->kv_heads;
-  const int keys_per_load = 64 / (p->head_dim / 8);
-  return p->partition_tokens == 0 && use_mfma(group) && p->block_size >= keys_per_load;
+  return p->partition_tokens == 0 && use_mfma(group);
 }
 
 int32_t decode_partition(const gk_decode_params* p) {

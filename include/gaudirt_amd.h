@@ -88,8 +88,7 @@ typedef struct gk_decode_params {
   int32_t sliding_window;      /* <= 0 = off */
   int32_t max_context;         /* host bound: row_context[r] <= max_context for every row */
   int32_t partition_tokens;    /* split-K partition (multiple of 32); 0 = library choice: for
-                                  GQA groups >= 4 and block_size >= 64 / (head_dim / 8) (4 at
-                                  head_dim 128, 8 at 64, 2 at 256) a balanced split of all
+                                  GQA groups >= 4 (any block_size) a balanced split of all
                                   key tiles over one resident grid, otherwise a partition
                                   sized from the batch */
   void* out;                   /* bf16 [rows, out_row_stride] */

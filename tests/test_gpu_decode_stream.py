@@ -1,8 +1,7 @@
 """GPU parity of the balanced decode schedule (gk_paged_decode with partition_tokens = 0).
 
-With the partition left to the library, GQA groups >= 4 and block_size >= the
-keys of one 16-byte load per lane (4 for head_dim 128, 8 for 64, 2 for 256),
-gk_paged_decode splits the batch's
+With the partition left to the library and GQA groups >= 4 (any block size,
+the token-granular map included), gk_paged_decode splits the batch's
 key tiles evenly over one resident grid: work units (row, kv head) are cut at
 arbitrary tiles, partial states are merged with the log-sum-exp rule, and the
 tiles of a unit are visited in rotated order. These cases pin every piece of
@@ -79,11 +78,12 @@ def test_stream_block_sizes(runner, block_size):
     check(case, runner.run_case(case))
 
 
-@pytest.mark.parametrize("geometry", [(128, 4), (128, 8), (128, 16), (64, 8), (64, 16), (256, 2), (256, 4),
-                                      (256, 8)])
+@pytest.mark.parametrize("geometry", [(128, 1), (128, 2), (128, 4), (128, 8), (128, 16), (64, 1), (64, 4),
+                                      (64, 8), (64, 16), (256, 1), (256, 2), (256, 4), (256, 8)])
 def test_stream_small_blocks(runner, geometry):
     # Blocks shorter than a tile: every 16-byte load of a tile (64 / (d / 8)
-    # keys) reads its own block-table entry.
+    # keys) reads its own block-table entry; shorter blocks, down to the
+    # token-granular map, one entry per key.
     d, block = geometry
     heads, kv_heads = (16, 2) if d == 256 else (32, 8)
     lens = np.array([1, 2, 3, 4, 5, 31, 33, 300, 777, 1024, 2047])
@@ -92,7 +92,7 @@ def test_stream_small_blocks(runner, geometry):
     check(case, runner.run_case(case))
 
 
-@pytest.mark.parametrize("block", [4, 16])
+@pytest.mark.parametrize("block", [1, 2, 4, 16])
 def test_stream_small_blocks_window_evicted(runner, block):
     # Sliding window over blocks shorter than a tile, with every slot outside
     # the visible keys poisoned (NaN) and the table entries of blocks wholly
@@ -118,18 +118,20 @@ def test_stream_small_blocks_window_evicted(runner, block):
 
 
 def test_library_choice_small_blocks(runner):
+    # Every block size takes the balanced schedule (partition 0) when the
+    # partition is left to the library and the GQA group is at least 4.
     import ctypes
     import torch
     from gaudirt_amd import capi
 
     lib = capi.load()
-    for d, block, stream in [(128, 4, True), (128, 2, False), (64, 8, True), (64, 4, False), (256, 2, True),
-                             (256, 1, False)]:
-        case = cases.decode_case(1, 2, 16, 2, d, block, 256, [30, 60])
+    for d, block, heads in [(128, 1, 16), (128, 2, 16), (64, 4, 16), (256, 1, 16), (128, 1, 6)]:
+        case = cases.decode_case(1, 2, heads, 2, d, block, 256, [30, 60])
         params = runner.decode_params(runner.bf16_device(case.query), runner.bf16_device(case.pool),
-                                      runner.to_device(case.block_tables), runner.to_device(case.lens), 16, 2, d,
-                                      block, case.scale, torch.empty(2, 16 * d, dtype=torch.bfloat16, device="cuda"))
-        assert (lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0) == stream, (d, block)
+                                      runner.to_device(case.block_tables), runner.to_device(case.lens), heads, 2, d,
+                                      block, case.scale, torch.empty(2, heads * d, dtype=torch.bfloat16, device="cuda"))
+        stream = heads // 2 >= 4
+        assert (lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0) == stream, (d, block, heads)
 
 
 def test_one_long_row_split_over_the_grid(runner):
