@@ -96,7 +96,9 @@ struct Cursor {
 
 // What consuming one tile needs (wave-uniform). The tile's keys fall into NR
 // runs of TS / NR keys, each inside one pool block: one run when blocks hold
-// at least TS keys, one run per 16-byte load of the tile otherwise.
+// at least TS keys, one run per 16-byte load of the tile when they hold at
+// least one load's keys (kKeyBlocks keeps no runs here: its per-key entries go
+// straight to the loads).
 template <int NR>
 struct TileDesc {
   int tb;                   // first key of the tile
