@@ -143,9 +143,16 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   const int wave_left_max =
       a.window > 0 ? pos_lo + min(nr - 1, (wave * kQrowsPerWave + kQrowsPerWave - 1) / g) - a.window + 1 : 0;
 
+  // At d 128 the V operands are read before the softmax (their LDS latency
+  // behind its arithmetic) and the row sums of the bf16 probabilities run on
+  // one more MFMA per step against an all-ones operand, in the output layout
+  // (rows 4q + r). At d 64 the registers these take would drop the kernel
+  // from four waves per SIMD to three, which costs more than they save: V is
+  // read next to its MFMAs and each lane sums its query row on the VALU
+  // (component 0 of l_run).
+  constexpr bool kEarlyV = D >= 128;
+  constexpr bool kMfmaSum = D >= 128;
   f32x4_t o[kNT][S::NO];
-  // Row sums of the bf16 probabilities, in the output layout (rows 4q + r),
-  // accumulated by one more MFMA per step against an all-ones operand.
   float m_run[kNT];
   f32x4_t l_run[kNT];
 #pragma unroll
@@ -245,17 +252,19 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       }
     }
 
-    // V operands of P . V (keys 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2), dims
-    // 16c + 4 (c16 & 3), read transposed), all issued before the softmax so
-    // that its arithmetic covers their LDS latency.
-    bf16x8_t vb[S::NO];
-#pragma unroll
-    for (int c = 0; c < S::NO; ++c) {
+    // V operand c of P . V: keys 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2),
+    // dims 16c + 4 (c16 & 3), read transposed.
+    auto read_v = [&](int c) {
       const int lc = 2 * c + ((c16 & 3) >> 1);
       const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
       const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3));
       const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3));
-      vb[c] = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+      return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    bf16x8_t vb[kEarlyV ? S::NO : 1];
+    if constexpr (kEarlyV) {
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) vb[c] = read_v(c);
     }
 
     // A step whose keys every valid query row of this wave sees (below the
@@ -300,13 +309,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
         const float m_new = fmaxf(m_run[nt], mx);
         const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
         m_run[nt] = m_new;
+        if constexpr (!kMfmaSum) l_run[nt][0] *= alpha;
         // o rows are qrows 4q + r; qrow h's factor lives in lanes with c16 == h.
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float f = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(alpha)));
 #pragma unroll
           for (int c = 0; c < S::NO; ++c) o[nt][c][r] *= f;
-          l_run[nt][r] *= f;
+          if constexpr (kMfmaSum) l_run[nt][r] *= f;
         }
       }
       const float base = m_run[nt] == -INFINITY ? 0.f : m_run[nt];
@@ -317,18 +327,25 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
         else ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) pa[nt][i] = (__bf16)ps[i];
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (!kMfmaSum) l_run[nt][0] += ps[i];
+        pa[nt][i] = (__bf16)ps[i];
+      }
     }
 
     // O[qrow][dim] += P . V, and the row sums.
 #pragma unroll
-    for (int c = 0; c < S::NO; ++c)
+    for (int c = 0; c < S::NO; ++c) {
+      const bf16x8_t v = kEarlyV ? vb[kEarlyV ? c : 0] : read_v(c);
 #pragma unroll
-      for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[nt], vb[c], o[nt][c]);
-    const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
-                           (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
+      for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[nt], v, o[nt][c]);
+    }
+    if constexpr (kMfmaSum) {
+      const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
+                             (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) l_run[nt] = mfma32(pa[nt], ones, l_run[nt]);
+      for (int nt = 0; nt < kNT; ++nt) l_run[nt] = mfma32(pa[nt], ones, l_run[nt]);
+    }
   };
 
   // kStages-deep pipeline over the workgroup, one barrier per step: before it
@@ -364,12 +381,16 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
     consume(kb0 + step * kKeys, kv[cur][0], kv[cur][1]);
   }
 
-  // Normalise and store: o row 4q + r of tile nt, its sum in l_run[nt][r].
+  // Normalise and store: o row 4q + r of tile nt, its sum in l_run[nt][r]
+  // (MFMA sums) or in lane c16 == 4q + r after the cross-row sum (VALU sums).
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
+    float l = 0.f;
+    if constexpr (!kMfmaSum) l = col4_sum(l_run[nt][0]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float lr = l_run[nt][r];
+      const float lr = kMfmaSum ? l_run[nt][r]
+                                : __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l)));
       const int qr = wave * kQrowsPerWave + nt * 16 + 4 * q + r;
       const int row = qr / g, head = qr % g;
       if (row >= nr) continue;
