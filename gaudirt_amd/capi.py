@@ -129,6 +129,14 @@ def load():
         return _lib
     if not LIB_PATH.exists():
         raise RuntimeError(f"{LIB_PATH} is missing: run `python -m gaudirt_amd.build` first")
+    # PyTorch-ROCm ships its own HIP runtime. Loading it first makes the library
+    # bind to that same runtime; loaded the other way round, the process holds
+    # two runtimes and launches on PyTorch's streams fail ("no ROCm-capable
+    # device is detected").
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(LIB_PATH))
     lib.gk_last_error.restype = ctypes.c_char_p
     lib.gk_version.restype = ctypes.c_char_p
