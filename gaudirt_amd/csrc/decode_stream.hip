@@ -167,9 +167,22 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       if (a.row_map) wmap = a.row_map[r];
     }
   };
+  // The contexts of the first kPre windows are loaded together (one memory
+  // round trip, not one per window); rows beyond them are read per window.
+  constexpr int kPre = 8;
+  int pctx[kPre];
+#pragma unroll
+  for (int k = 0; k < kPre; ++k) {
+    const int r = 64 * k + lane;
+    pctx[k] = r < a.rows ? a.row_context[r] : 0;
+  }
   load_window(0);
-  int64_t total = wave_sum(lane < a.rows ? row_tiles<TS>(wctx, a.window).count : 0, lane);
-  for (int base = 64; base < a.rows; base += 64) {
+  int lane_tiles = 0;
+#pragma unroll
+  for (int k = 0; k < kPre; ++k)
+    if (64 * k + lane < a.rows) lane_tiles += row_tiles<TS>(pctx[k], a.window).count;
+  int64_t total = wave_sum(lane_tiles, lane);
+  for (int base = 64 * kPre; base < a.rows; base += 64) {
     const int r = base + lane;
     total += wave_sum(r < a.rows ? row_tiles<TS>(a.row_context[r], a.window).count : 0, lane);
   }
@@ -184,8 +197,24 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   int64_t row_base = 0;
   int64_t pre = 0;
   bool found = false;
-  for (int base = 0; base < a.rows; base += 64) {
-    if (base != wb) load_window(base);
+#pragma unroll
+  for (int k = 0; k < kPre; ++k) {
+    if (found || 64 * k >= a.rows) continue;
+    const int r = 64 * k + lane;
+    const int n = r < a.rows ? row_tiles<TS>(pctx[k], a.window).count : 0;
+    const int incl = wave_inclusive_scan(n, lane);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(r < a.rows && (pre + incl) * U > g_begin);
+    if (hit) {
+      const int f = __builtin_ctzll(hit);
+      row = 64 * k + f;
+      row_base = (pre + __builtin_amdgcn_readlane(incl - n, f)) * U;
+      found = true;
+    } else {
+      pre += __builtin_amdgcn_readlane(incl, 63);
+    }
+  }
+  for (int base = 64 * kPre; !found && base < a.rows; base += 64) {
+    load_window(base);
     const int r = base + lane;
     const int n = r < a.rows ? row_tiles<TS>(wctx, a.window).count : 0;
     const int incl = wave_inclusive_scan(n, lane);
@@ -195,11 +224,12 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       row = base + f;
       row_base = (pre + __builtin_amdgcn_readlane(incl - n, f)) * U;
       found = true;
-      break;
+    } else {
+      pre += __builtin_amdgcn_readlane(incl, 63);
     }
-    pre += __builtin_amdgcn_readlane(incl, 63);
   }
   if (!found) return;  // unreachable: g_begin < total
+  if ((row & ~63) != wb) load_window(row & ~63);
 
   // A new unit's kv head and the rotation of its tile order.
   auto enter_unit = [&](Cursor& c) {

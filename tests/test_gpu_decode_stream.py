@@ -151,6 +151,15 @@ def test_many_rows_skewed(runner):
     check(case, runner.run_case(case))
 
 
+def test_rows_beyond_the_prefetched_windows(runner):
+    # 700 rows: the schedule reads the first 512 rows' contexts in one batch
+    # and the rest 64 rows at a time; workgroups start in both parts.
+    rng = np.random.default_rng(17)
+    lens = rng.integers(1, 400, 700).astype(np.int32)
+    case = cases.decode_case(24, len(lens), 8, 2, 64, 16, int(((lens + 15) // 16).sum()) + 8, lens)
+    check(case, runner.run_case(case))
+
+
 def test_tiny_batch_fewer_tiles_than_workgroups(runner):
     case = cases.decode_case(23, 2, 8, 2, 128, 64, 8, [3, 40])
     check(case, runner.run_case(case))
