@@ -129,7 +129,7 @@ def host_cpu():
 
 
 def prefill_bench(args):
-    """one gk_paged_prefill call per step; MFMA roofline (causal-exact FLOPs)."""
+    """Workload C4: one gk_paged_prefill call per step; MFMA roofline (causal-exact FLOPs)."""
     import torch
 
     from gaudirt_amd import capi, workloads

@@ -1,6 +1,6 @@
 """Seeded synthetic workloads of the benchmark configurations.
 
-The BASELINE configurations in block-table form: a bf16 head-major pool
+The benchmark workloads C1-C5 in block-table form: a bf16 head-major pool
 [2, Hkv, S, d] filled with N(0, 1), query rows, seeded non-overlapping block
 tables and seeded lengths. Generated on the GPU with a seeded torch generator.
 """
@@ -111,7 +111,7 @@ class DeviceDecodeCase:
 
 
 class DevicePrefillCase:
-    """BASELINE config 3 on the GPU: prefix-shared chunked prefill.
+    """Workload C4 on the GPU: prefix-shared chunked prefill.
 
     `seqs` sequences share a `prefix`-token prefix through identical block ids
     (the first prefix/block blocks of every table), each adds `chunk` causal

@@ -63,7 +63,7 @@ def decode_case(seed, batch, heads, kv_heads, head_dim, block_size, num_blocks, 
 
 
 def c1_case(seed=20261201):
-    """batch 4, 8 q / 2 kv heads, d 128, block 128, ctx U[1,512], 64-block pool."""
+    """Workload C1: batch 4, 8 q / 2 kv heads, d 128, block 128, ctx U[1,512], 64-block pool."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(1, 513, 4)
     return decode_case(seed + 1, 4, 8, 2, 128, 128, 64, lens)

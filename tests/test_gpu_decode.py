@@ -1,6 +1,6 @@
 """GPU parity of the decode path (C ABI) against the CPU oracle.
 
-Tolerance: bf16 outputs within max-abs 2e-2 and mean-abs
+Tolerance (the benchmark's parity gate): bf16 outputs within max-abs 2e-2 and mean-abs
 2e-3 of the reference implementation (direct_bf16_pv, and tiled_bf16_pv with
 the reference's 512-key tile), plus the reference's own relative-L2 gates
 (<= 1e-2 vs fp64, <= 5e-3 vs tiled; tests/paged_attention_reference.py:60-69).

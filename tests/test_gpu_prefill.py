@@ -6,7 +6,7 @@ against a single-row decode on the same prefix
 (tests/paged_attention_prefix_equivalence_smoke.py), GQA geometries, sliding
 window / softcap (tests/paged_attention_generalized_smoke.py) and poisoned
 unused slots (tests/multitile_paged_attention_unit_test.cpp:1722-1767).
-BASELINE config 3 (8 x 512-row chunks on a shared 2048-token prefix) is run at
+Workload C4 (8 x 512-row chunks on a shared 2048-token prefix) is run at
 full size and checked on sampled rows plus the cross-path property.
 """
 
@@ -125,7 +125,7 @@ def test_prefill_rejects_bad_blocks(runner):
 
 
 def test_c4_prefix_shared_chunked_prefill(runner):
-    """BASELINE config 3 at full size: 8 sequences, shared 2048-token prefix
+    """Workload C4 at full size: 8 sequences, shared 2048-token prefix
     (identical block ids 0..15 of the pool), 512-row causal chunks, 32 q / 8 kv
     heads, d 128. Sampled rows against the oracle; every chunk's last row
     against a single-row decode over the same prefix (cross-path property)."""
