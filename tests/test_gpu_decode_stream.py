@@ -165,10 +165,11 @@ def test_tiny_batch_fewer_tiles_than_workgroups(runner):
     check(case, runner.run_case(case))
 
 
+@pytest.mark.parametrize("block", [1, 4, 32])
 @pytest.mark.parametrize("variant", ["window", "softcap", "both"])
-def test_stream_window_and_softcap(runner, variant):
+def test_stream_window_and_softcap(runner, variant, block):
     lens = np.array([40, 300, 1000, 64, 65, 3000, 1])
-    case = cases.decode_case(31, len(lens), 16, 4, 128, 32, 512, lens)
+    case = cases.decode_case(31, len(lens), 16, 4, 128, block, 16384 // block, lens)
     if variant in ("window", "both"):
         case.window = 77  # starts inside a 32-key tile
     if variant in ("softcap", "both"):

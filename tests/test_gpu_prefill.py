@@ -96,9 +96,10 @@ def test_prefill_shared_prefix_small(runner):
     check(case, runner.run_prefill_case(case))
 
 
+@pytest.mark.parametrize("block", [1, 4, 32])
 @pytest.mark.parametrize("variant", ["window", "softcap"])
-def test_prefill_window_and_softcap(runner, variant):
-    case = cases.PrefillCase(9, 16, 4, 128, 32, prefixes=[100, 0, 333], chunks=[90, 200, 17],
+def test_prefill_window_and_softcap(runner, variant, block):
+    case = cases.PrefillCase(9, 16, 4, 128, block, prefixes=[100, 0, 333], chunks=[90, 200, 17],
                              softcap=40.0 if variant == "softcap" else 0.0,
                              window=70 if variant == "window" else -1)
     check(case, runner.run_prefill_case(case), fp32_softmax=True)
