@@ -150,6 +150,42 @@ static inline float qk(const uint16_t* q, const uint16_t* k, int32_t d) {
   return acc;
 }
 
+/* qk() for keys rows[0 .. n): out[t] = qk(q, rows[t], d), every key summed in
+ * the same order (c = 0, 1, ...) with the same roundings. Eight keys run as
+ * independent chains at a time, which only changes how fast the sums are
+ * formed, not their values. */
+#define ORC_KEYS 8
+static void qk_keys(const uint16_t* q, const uint16_t* const* rows, int64_t n, int32_t d, float* out) {
+  int64_t t = 0;
+  for (; t + ORC_KEYS <= n; t += ORC_KEYS) {
+    float acc[ORC_KEYS] = {0.f};
+    for (int32_t c = 0; c < d; ++c) {
+      const float qc = orc_bf16_to_f32(q[c]);
+      for (int j = 0; j < ORC_KEYS; ++j) acc[j] += qc * orc_bf16_to_f32(rows[t + j][c]);
+    }
+    for (int j = 0; j < ORC_KEYS; ++j) out[t + j] = acc[j];
+  }
+  for (; t < n; ++t) out[t] = qk(q, rows[t], d);
+}
+
+/* The binary64 form: out[t] = sum_c (double)q[c] * (double)k[c], in order. */
+static void qk_keys64(const uint16_t* q, const uint16_t* const* rows, int64_t n, int32_t d, double* out) {
+  int64_t t = 0;
+  for (; t + ORC_KEYS <= n; t += ORC_KEYS) {
+    double acc[ORC_KEYS] = {0.0};
+    for (int32_t c = 0; c < d; ++c) {
+      const double qc = (double)orc_bf16_to_f32(q[c]);
+      for (int j = 0; j < ORC_KEYS; ++j) acc[j] += qc * (double)orc_bf16_to_f32(rows[t + j][c]);
+    }
+    for (int j = 0; j < ORC_KEYS; ++j) out[t + j] = acc[j];
+  }
+  for (; t < n; ++t) {
+    double s = 0.0;
+    for (int32_t c = 0; c < d; ++c) s += (double)orc_bf16_to_f32(q[c]) * (double)orc_bf16_to_f32(rows[t][c]);
+    out[t] = s;
+  }
+}
+
 static inline float apply_softcap(float s, float cap) {
   return cap > 0.f ? cap * tanhf(s / cap) : s;
 }
@@ -173,12 +209,13 @@ static const uint16_t* value_row(const orc_attention_args* a, int32_t kvh, int32
  * fp32 scores times scale, one fp32 softmax, probabilities rounded to bf16,
  * fp32 P.V, bf16 output. */
 static void direct_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots,
-                       int64_t n, float* scores, float* acc, uint16_t* out) {
+                       const uint16_t* const* krows, int64_t n, float* scores, float* acc, uint16_t* out) {
   const int32_t d = a->head_dim, kvh = h / (a->heads / a->kv_heads);
   const uint16_t* q = a->query + row * a->q_stride + (int64_t)h * d;
+  qk_keys(q, krows, n, d, scores);
   float m = -INFINITY;
   for (int64_t t = 0; t < n; ++t) {
-    scores[t] = apply_softcap(qk(q, key_row(a, kvh, slots[t]), d) * a->scale, a->softcap);
+    scores[t] = apply_softcap(scores[t] * a->scale, a->softcap);
     if (scores[t] > m) m = scores[t];
   }
   float sum = 0.f;
@@ -199,15 +236,17 @@ static void direct_row(const orc_attention_args* a, int64_t row, int32_t h, cons
  * Per-tile max and sum, per-tile normalised bf16 probabilities, fp32 running
  * (max, sum, output) merge, bf16 output. */
 static void tiled_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots,
-                      int64_t n, int32_t tile, float* scores, float* acc, float* run, uint16_t* out) {
+                      const uint16_t* const* krows, int64_t n, int32_t tile, float* dots, float* scores,
+                      float* acc, float* run, uint16_t* out) {
   const int32_t d = a->head_dim, kvh = h / (a->heads / a->kv_heads);
   const uint16_t* q = a->query + row * a->q_stride + (int64_t)h * d;
+  qk_keys(q, krows, n, d, dots);
   float run_max = 0.f, run_sum = 0.f;
   for (int64_t start = 0; start < n; start += tile) {
     const int64_t count = (n - start < tile) ? n - start : tile;
     float tmax = -INFINITY;
     for (int64_t t = 0; t < count; ++t) {
-      scores[t] = apply_softcap(qk(q, key_row(a, kvh, slots[start + t]), d) * a->scale, a->softcap);
+      scores[t] = apply_softcap(dots[start + t] * a->scale, a->softcap);
       if (scores[t] > tmax) tmax = scores[t];
     }
     float tsum = 0.f;
@@ -242,13 +281,14 @@ static void tiled_row(const orc_attention_args* a, int64_t row, int32_t h, const
  * Global max and denominator, per-tile unnormalised bf16 probabilities scaled
  * by exp(local_max - max). */
 static void direct_tiled_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots,
-                             int64_t n, int32_t tile, float* scores, float* acc, float* num,
-                             uint16_t* out) {
+                             const uint16_t* const* krows, int64_t n, int32_t tile, float* scores, float* acc,
+                             float* num, uint16_t* out) {
   const int32_t d = a->head_dim, kvh = h / (a->heads / a->kv_heads);
   const uint16_t* q = a->query + row * a->q_stride + (int64_t)h * d;
+  qk_keys(q, krows, n, d, scores);
   float m = -INFINITY;
   for (int64_t t = 0; t < n; ++t) {
-    scores[t] = apply_softcap(qk(q, key_row(a, kvh, slots[t]), d) * a->scale, a->softcap);
+    scores[t] = apply_softcap(scores[t] * a->scale, a->softcap);
     if (scores[t] > m) m = scores[t];
   }
   float den = 0.f;
@@ -274,16 +314,14 @@ static void direct_tiled_row(const orc_attention_args* a, int64_t row, int32_t h
 /* binary64 attention for one (row, head): the fp64 truth of
  * tests/paged_attention_smoke.py:39-50 and
  * tests/fused_paged_decode_device_test.cpp:374-440 (before direct_bf16). */
-static void fp64_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots, int64_t n,
-                     double* scores, double* out) {
+static void fp64_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots,
+                     const uint16_t* const* krows, int64_t n, double* scores, double* out) {
   const int32_t d = a->head_dim, kvh = h / (a->heads / a->kv_heads);
   const uint16_t* q = a->query + row * a->q_stride + (int64_t)h * d;
+  qk_keys64(q, krows, n, d, scores);
   double m = -INFINITY;
   for (int64_t t = 0; t < n; ++t) {
-    const uint16_t* k = key_row(a, kvh, slots[t]);
-    double s = 0.0;
-    for (int32_t c = 0; c < d; ++c) s += (double)orc_bf16_to_f32(q[c]) * (double)orc_bf16_to_f32(k[c]);
-    s *= (double)a->scale;
+    double s = scores[t] * (double)a->scale;
     if (a->softcap > 0.f) s = (double)a->softcap * tanh(s / (double)a->softcap);
     scores[t] = s;
     if (s > m) m = s;
@@ -303,13 +341,14 @@ static void fp64_row(const orc_attention_args* a, int64_t row, int32_t h, const 
 
 /* fp32 softmax without bf16 probabilities: the CPU reference of
  * tests/paged_attention_generalized_smoke.py:16-34 (softcap and sliding window). */
-static void fp32_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots, int64_t n,
-                     float* scores, float* acc, uint16_t* out) {
+static void fp32_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots,
+                     const uint16_t* const* krows, int64_t n, float* scores, float* acc, uint16_t* out) {
   const int32_t d = a->head_dim, kvh = h / (a->heads / a->kv_heads);
   const uint16_t* q = a->query + row * a->q_stride + (int64_t)h * d;
+  qk_keys(q, krows, n, d, scores);
   float m = -INFINITY;
   for (int64_t t = 0; t < n; ++t) {
-    scores[t] = apply_softcap(qk(q, key_row(a, kvh, slots[t]), d) * a->scale, a->softcap);
+    scores[t] = apply_softcap(scores[t] * a->scale, a->softcap);
     if (scores[t] > m) m = scores[t];
   }
   float sum = 0.f;
@@ -333,14 +372,16 @@ static void fp32_row(const orc_attention_args* a, int64_t row, int32_t h, const 
  *   with prev_unscaled on the second tile, gk_attn_online_finalize_bf16_v1
  *   (same file, :1425-1480 and the emulation at :628-738). Tiles beyond the
  *   row's position are empty (m = -inf, l = 0) and merge as no-ops. */
-static void guid_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots, int64_t n,
-                     int32_t tiles, int32_t tile, float* scores, float* acc, float* run, uint16_t* out) {
+static void guid_row(const orc_attention_args* a, int64_t row, int32_t h, const int32_t* slots,
+                     const uint16_t* const* krows, int64_t n, int32_t tiles, int32_t tile, float* dots,
+                     float* scores, float* acc, float* run, uint16_t* out) {
   const int32_t d = a->head_dim, kvh = h / (a->heads / a->kv_heads);
   const uint16_t* q = a->query + row * a->q_stride + (int64_t)h * d;
+  qk_keys(q, krows, n, d, dots);
   if (tiles <= 1) {
     float m = -INFINITY;
     for (int64_t t = 0; t < n; ++t) {
-      scores[t] = qk(q, key_row(a, kvh, slots[t]), d) * a->scale;
+      scores[t] = dots[t] * a->scale;
       if (scores[t] > m) m = scores[t];
     }
     const float origin = isinf(m) ? 0.f : m;
@@ -369,7 +410,7 @@ static void guid_row(const orc_attention_args* a, int64_t row, int32_t h, const 
     for (int32_t c = 0; c < d; ++c) acc[c] = 0.f;
     if (last >= 0) {
       for (int64_t k = 0; k <= last; ++k) {
-        scores[k] = qk(q, key_row(a, kvh, slots[key_start + k]), d) * a->scale;
+        scores[k] = dots[key_start + k] * a->scale;
         if (scores[k] > tm) tm = scores[k];
       }
       const float origin = (tm == -INFINITY) ? 0.f : tm;
@@ -413,12 +454,14 @@ static void* attention_worker(void* opaque) {
   const int64_t max_keys = a->context;
   int32_t* slots = (int32_t*)malloc(sizeof(int32_t) * (size_t)(max_keys > 0 ? max_keys : 1));
   float* scores = (float*)malloc(sizeof(float) * (size_t)(max_keys > 0 ? max_keys : 1));
+  float* dots = (float*)malloc(sizeof(float) * (size_t)(max_keys > 0 ? max_keys : 1));
   double* scores64 = (double*)malloc(sizeof(double) * (size_t)(max_keys > 0 ? max_keys : 1));
+  const uint16_t** krows = (const uint16_t**)malloc(sizeof(uint16_t*) * (size_t)(max_keys > 0 ? max_keys : 1));
   float* acc = (float*)malloc(sizeof(float) * (size_t)d * 2);
   float* run = acc + d;
-  if (!slots || !scores || !scores64 || !acc) {
+  if (!slots || !scores || !dots || !scores64 || !krows || !acc) {
     w->status = -2;
-    free(slots); free(scores); free(scores64); free(acc);
+    free(slots); free(scores); free(dots); free(scores64); free(krows); free(acc);
     return NULL;
   }
   const int64_t items = a->rows * a->kv_heads;
@@ -430,23 +473,26 @@ static void* attention_worker(void* opaque) {
     if (pos < 0 || pos >= a->context) { w->status = -3; break; }
     const int64_t n = pos - left + 1;
     const int32_t* map_row = a->mapping + a->requests[row] * a->context;
-    for (int64_t t = 0; t < n; ++t) slots[t] = map_row[left + t];
+    for (int64_t t = 0; t < n; ++t) {
+      slots[t] = map_row[left + t];
+      krows[t] = key_row(a, kvh, slots[t]);
+    }
     for (int32_t gh = 0; gh < group; ++gh) {
       const int32_t h = kvh * group + gh;
       uint16_t* o16 = w->out16 ? w->out16 + (row * a->heads + h) * d : NULL;
       switch (w->kind) {
-        case 0: direct_row(a, row, h, slots, n, scores, acc, o16); break;
-        case 1: tiled_row(a, row, h, slots, n, w->kv_tile, scores, acc, run, o16); break;
-        case 2: direct_tiled_row(a, row, h, slots, n, w->kv_tile, scores, acc, run, o16); break;
-        case 3: fp64_row(a, row, h, slots, n, scores64, w->out64 + (row * a->heads + h) * d); break;
-        case 4: fp32_row(a, row, h, slots, n, scores, acc, o16); break;
+        case 0: direct_row(a, row, h, slots, krows, n, scores, acc, o16); break;
+        case 1: tiled_row(a, row, h, slots, krows, n, w->kv_tile, dots, scores, acc, run, o16); break;
+        case 2: direct_tiled_row(a, row, h, slots, krows, n, w->kv_tile, scores, acc, run, o16); break;
+        case 3: fp64_row(a, row, h, slots, krows, n, scores64, w->out64 + (row * a->heads + h) * d); break;
+        case 4: fp32_row(a, row, h, slots, krows, n, scores, acc, o16); break;
         default:
-          guid_row(a, row, h, slots, n, w->tiles_per_row[row], w->kv_tile, scores, acc, run, o16);
+          guid_row(a, row, h, slots, krows, n, w->tiles_per_row[row], w->kv_tile, dots, scores, acc, run, o16);
           break;
       }
     }
   }
-  free(slots); free(scores); free(scores64); free(acc);
+  free(slots); free(scores); free(dots); free(scores64); free(krows); free(acc);
   return NULL;
 }
 

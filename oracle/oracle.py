@@ -219,10 +219,22 @@ class Problem:
         return np.zeros((self.query.shape[0], self.heads * self.head_dim), dtype=np.uint16)
 
 
+def host_threads():
+    """Threads for the attention references: every CPU this process may run on
+    (its affinity mask), bounded by OMP_NUM_THREADS when the host sets it to
+    the process's CPU share."""
+    try:
+        cpus = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        cpus = os.cpu_count() or 1
+    limit = os.environ.get("OMP_NUM_THREADS", "")
+    if limit.isdigit() and int(limit) > 0:
+        cpus = min(cpus, int(limit))
+    return max(1, cpus)
+
+
 def _threads(threads):
-    if threads is None:
-        return max(1, min(16, os.cpu_count() or 1))
-    return threads
+    return host_threads() if threads is None else threads
 
 
 def _check(status):
@@ -368,6 +380,15 @@ def check_tolerance(actual_bits, reference_bits, max_abs=2e-2, mean_abs=2e-3):
         f"> bound {bound.flat[worst]}")
     assert diff.mean() <= mean_abs, (float(diff.mean()), mean_abs)
     return float(diff.max()), float(diff.mean())
+
+
+def ulp_allowance_count(actual_bits, reference_bits, max_abs=2e-2):
+    """Elements within one bf16 ulp of the reference but farther than the flat max_abs:
+    those that pass check_tolerance only through its ulp allowance."""
+    a = bf16_to_f32(actual_bits).astype(np.float64)
+    b = bf16_to_f32(reference_bits).astype(np.float64)
+    diff = np.abs(a - b)
+    return int(((diff > max_abs) & (diff <= bf16_ulp(b))).sum())
 
 
 # ---------------------------------------------------------------------------

@@ -1,0 +1,139 @@
+"""GPU parity of long-context chunked prefill against the CPU oracle.
+
+The reference's multi-tile cases (tests/multitile_paged_attention_unit_test.cpp:
+1642-1655: 14 q / 2 kv heads, head_dim 64, 12288-slot pool, N(0, 0.5) data,
+the slot table reversed so consecutive tokens sit in descending slots) run
+through the drop-in op torch.ops.gaudirt.paged_attn (store, then prefill over
+the token-granular map); the 28672 + 4096 = 32768-key chunk of the same file
+(:1586-1598, 56 q / 8 kv heads, head_dim 128) runs through the C ABI with
+128-token blocks; workload C4 is checked on every row. Each case checks every
+listed row against direct_bf16_pv (max-abs 2e-2, mean-abs 2e-3), the
+relative-L2 gates against fp64 (1e-2) and tiled_bf16_pv (5e-3), and prints the
+worst errors and how many elements passed only through the one-ulp allowance
+of the output gate.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import paged_cases as cases
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+@pytest.fixture(scope="module")
+def torch_ext():
+    import torch
+
+    import gaudirt_amd
+
+    assert torch.cuda.is_available()
+    gaudirt_amd.load_extension()
+    return torch
+
+
+def report(name, actual, problem):
+    """Every gate of the prefill parity on these rows; prints the figures."""
+    direct = orc.direct_bf16_pv(problem)
+    assert np.isfinite(orc.bf16_to_f32(actual)).all()
+    max_abs, mean_abs = orc.check_tolerance(actual, direct, MAX_ABS, MEAN_ABS)
+    ulp_only = orc.ulp_allowance_count(actual, direct, MAX_ABS)
+    tiled = orc.tiled_bf16_pv(problem, 512)
+    e64, etiled = orc.isolated_errors(orc.bf16_to_f32(actual), orc.fp64_bf16(problem), orc.bf16_to_f32(tiled))
+    print(f"{name}: rows={actual.shape[0]} max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} "
+          f"ulp_allowance_only={ulp_only} of {actual.size} fp64_rel_l2={e64:.3e} tiled_rel_l2={etiled:.3e}",
+          flush=True)
+    return max_abs, mean_abs, ulp_only
+
+
+def boundary_rows(rows, tile_sizes, every=0):
+    """First and last row of every tile for each tile size (the work-tile edges
+    of the prefill kernel's row tiling), optionally every `every`-th row."""
+    sel = set()
+    for t in tile_sizes:
+        for first in range(0, rows, t):
+            sel.add(first)
+            sel.add(min(rows, first + t) - 1)
+    if every:
+        sel.update(range(0, rows, every))
+    return np.array(sorted(sel))
+
+
+def bf16_bits(torch, t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("prefix,rows", [(0, 1024), (3840, 263), (5300, 197), (8300, 229)])
+def test_reference_multitile_cases(torch_ext, prefix, rows):
+    import gaudirt_amd
+
+    torch = torch_ext
+    heads, kv_heads, dim, slots, context = 14, 2, 64, 12288, 16384
+    total = prefix + rows
+    slot_table = (1 + (total - 1 - np.arange(total))).astype(np.int32)
+    mapping = np.full((1, context), -1, dtype=np.int32)
+    mapping[0, :total] = slot_table
+    rng = np.random.default_rng(20261110 + prefix)
+
+    def normal_half(shape):
+        return orc.bf16_from_f32((0.5 * rng.standard_normal(shape)).astype(np.float32))
+
+    base = np.zeros((2, kv_heads, slots, dim), dtype=np.uint16)
+    base[:, :, slot_table[:prefix], :] = normal_half((2, kv_heads, prefix, dim))
+    q, k, v = normal_half((rows, heads * dim)), normal_half((rows, kv_heads * dim)), normal_half((rows, kv_heads * dim))
+    requests = np.zeros(rows, dtype=np.int64)
+    positions = prefix + np.arange(rows, dtype=np.int64)
+    locations = slot_table[positions].astype(np.int64)
+    meta = torch.classes.gaudirt.PagedMetadata(torch.from_numpy(locations), torch.from_numpy(requests),
+                                               torch.from_numpy(positions), torch.from_numpy(mapping), slots)
+
+    def dev(bits):
+        return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+    pool = gaudirt_amd.allocate_paged_kv(1, slots, kv_heads, dim)
+    pool[0].copy_(dev(base))
+    key_pool, value_pool = gaudirt_amd.kv_pool_views(pool, 0)
+    scale = float(np.float32(1 / math.sqrt(dim)))
+    print(f"multitile case prefix={prefix} rows={rows}", flush=True)
+    out = torch.ops.gaudirt.paged_attn.default(dev(q), dev(k), dev(v), key_pool, value_pool, meta, dim, scale)
+    torch.cuda.synchronize()
+    expected = base.copy()
+    orc.kv_store(k, v, locations, rows, expected, slots, kv_heads, dim)
+    assert np.array_equal(bf16_bits(torch, pool[0]), expected), "KV store differs from the oracle"
+    problem = orc.Problem(q, expected, requests, positions, mapping, heads, kv_heads, dim, scale)
+    report(f"multitile prefix={prefix} rows={rows}", bf16_bits(torch, out), problem)
+
+
+@pytest.mark.timeout(300)
+def test_long_prefill_32k_chunk(torch_ext):
+    """28672-token cached prefix + a 4096-row causal chunk (32768 keys for the
+    last row), 56 q / 8 kv heads (GQA 7), head_dim 128, 128-token blocks. Rows
+    checked: the first and last of every 18-row work tile (128 (row, head)
+    pairs per workgroup at GQA 7) and every 128th row."""
+    from tests import gk_runner
+
+    torch = torch_ext
+    case = cases.PrefillCase(32768, 56, 8, 128, 128, prefixes=[28672], chunks=[4096])
+    print("32k prefill: pool slots", case.slots, flush=True)
+    actual = gk_runner.run_prefill_case(case)
+    sel = boundary_rows(case.rows, tile_sizes=(128 // 7,), every=128)
+    report("prefill 28672+4096", actual[sel], case.oracle_problem(sel))
+    del torch
+
+
+@pytest.mark.timeout(300)
+def test_c4_every_row(torch_ext):
+    """Workload C4 at full size, every one of its 4096 rows (32 q / 8 kv heads,
+    8 x 512-row chunks on a shared 2048-token prefix, head_dim 128)."""
+    from tests import gk_runner
+
+    torch = torch_ext
+    case = cases.PrefillCase(2026, 32, 8, 128, 128, prefixes=[2048] * 8, chunks=[512] * 8, shared_prefix_blocks=16)
+    actual = gk_runner.run_prefill_case(case)
+    report("c4 all rows", actual, case.oracle_problem())
+    del torch
