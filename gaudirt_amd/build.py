@@ -29,7 +29,7 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", str(ROOT / "include"), "-I", str(CSRC),
           "-Wall", "-Wno-unused-function"]
 
-LIB_SOURCES = ["gk_api.cpp", "block_allocator.cpp", "kv_store.hip", "paged_decode.hip", "decode_stream.hip",
+LIB_SOURCES = ["gk_api.cpp", "block_allocator_core.cpp", "block_allocator.cpp", "kv_store.hip", "paged_decode.hip", "decode_stream.hip",
                "paged_prefill.hip", "metadata.hip", "rotary.hip"]
 LIB_NAME = "libgaudirt_amd.so"
 
