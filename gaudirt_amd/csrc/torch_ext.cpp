@@ -29,6 +29,7 @@
 #include <limits>
 #include <memory>
 #include <mutex>
+#include <numeric>
 #include <unordered_map>
 #include <vector>
 
@@ -231,49 +232,68 @@ class PagedMetadata : public torch::CustomClassHolder {
                     context <= std::numeric_limits<int32_t>::max() &&
                     mapping.numel() <= std::numeric_limits<int32_t>::max(),
                 "GaudiRT: paged metadata dimensions outside supported range");
-    const auto read = [](const at::Tensor& t, int64_t i) -> int64_t {
-      return t.scalar_type() == at::kInt ? t.data_ptr<int32_t>()[i] : t.data_ptr<int64_t>()[i];
-    };
-    mapping_h_.resize(mapping.numel());
-    for (int64_t i = 0; i < mapping.numel(); ++i) {
-      const auto slot = read(mapping, i);
-      TORCH_CHECK(slot >= -1 && slot < slots, "GaudiRT: request-to-token slot is out of range");
-      mapping_h_[i] = static_cast<int32_t>(slot);
-    }
-    locations_h_.resize(m);
-    requests_h_.resize(m);
-    positions_h_.resize(m);
-    max_position_.assign(request_count, -1);
-    std::unordered_map<int32_t, std::pair<int32_t, int32_t>> targets;
-    targets.reserve(m * 2);
+    // Whole-tensor checks first, then one failure code per row; the first
+    // failing row reports its first failing check, so the messages and their
+    // order are those of the reference's row-by-row scan.
+    const auto map64 = mapping.to(at::kLong);
+    TORCH_CHECK(map64.ge(-1).all().item<bool>() && map64.lt(slots).all().item<bool>(),
+                "GaudiRT: request-to-token slot is out of range");
+    const auto map32 = map64.to(at::kInt);
+    mapping_h_.assign(map32.data_ptr<int32_t>(), map32.data_ptr<int32_t>() + map32.numel());
+    const auto loc = locations.to(at::kLong), req = requests.to(at::kLong), pos = positions.to(at::kLong);
+    const int64_t* loc_p = loc.data_ptr<int64_t>();
+    const int64_t* req_p = req.data_ptr<int64_t>();
+    const int64_t* pos_p = pos.data_ptr<int64_t>();
+    enum RowFault : int { kRowOk = 0, kRowRange, kRowMismatch, kRowDuplicate };
+    std::vector<int> fault(m, kRowOk);
     for (int64_t i = 0; i < m; ++i) {
-      const auto slot = read(locations, i), request = read(requests, i), position = read(positions, i);
-      TORCH_CHECK(slot >= 0 && slot < slots && request >= 0 && request < request_count && position >= 0 &&
-                      position < context,
-                  "GaudiRT: paged metadata index is out of range");
-      TORCH_CHECK(mapping_h_[request * context + position] == slot,
-                  "GaudiRT: output slot does not match request-to-token mapping");
-      const bool inserted =
-          targets.emplace(static_cast<int32_t>(slot), std::make_pair(static_cast<int32_t>(request),
-                                                                     static_cast<int32_t>(position)))
-              .second;
-      TORCH_CHECK(inserted, "GaudiRT: duplicate output KV slot");
-      locations_h_[i] = static_cast<int32_t>(slot);
-      requests_h_[i] = static_cast<int32_t>(request);
-      positions_h_[i] = static_cast<int32_t>(position);
-      if (i == 0 || requests_h_[i - 1] != request || positions_h_[i - 1] + 1 != position)
-        sequences_.push_back({static_cast<int32_t>(i), 1, static_cast<int32_t>(position)});
-      else
-        ++sequences_.back().length;
-      max_position_[request] = std::max(max_position_[request], static_cast<int32_t>(position));
+      if (loc_p[i] < 0 || loc_p[i] >= slots || req_p[i] < 0 || req_p[i] >= request_count || pos_p[i] < 0 ||
+          pos_p[i] >= context)
+        fault[i] = kRowRange;
+      else if (mapping_h_[req_p[i] * context + pos_p[i]] != loc_p[i])
+        fault[i] = kRowMismatch;
     }
+    // Output slots sorted with their row: a slot's rows after its first are
+    // duplicates, and the sorted list answers "which row writes slot s" below.
+    std::vector<int64_t> by_slot(m);
+    std::iota(by_slot.begin(), by_slot.end(), int64_t{0});
+    std::sort(by_slot.begin(), by_slot.end(),
+              [&](int64_t a, int64_t b) { return loc_p[a] != loc_p[b] ? loc_p[a] < loc_p[b] : a < b; });
+    for (int64_t k = 1; k < m; ++k)
+      if (loc_p[by_slot[k]] == loc_p[by_slot[k - 1]] && fault[by_slot[k]] == kRowOk) fault[by_slot[k]] = kRowDuplicate;
+    const auto bad = std::find_if(fault.begin(), fault.end(), [](int f) { return f != kRowOk; });
+    if (bad != fault.end()) {
+      TORCH_CHECK(*bad != kRowRange, "GaudiRT: paged metadata index is out of range");
+      TORCH_CHECK(*bad != kRowMismatch, "GaudiRT: output slot does not match request-to-token mapping");
+      TORCH_CHECK(false, "GaudiRT: duplicate output KV slot");
+    }
+    locations_h_.assign(loc_p, loc_p + m);
+    requests_h_.assign(req_p, req_p + m);
+    positions_h_.assign(pos_p, pos_p + m);
+    // Runs of consecutive positions of one request, from their boundaries.
+    std::vector<int32_t> run_starts;
+    for (int64_t i = 0; i < m; ++i)
+      if (i == 0 || requests_h_[i] != requests_h_[i - 1] || positions_h_[i] != positions_h_[i - 1] + 1)
+        run_starts.push_back(static_cast<int32_t>(i));
+    run_starts.push_back(static_cast<int32_t>(m));
+    for (size_t k = 0; k + 1 < run_starts.size(); ++k)
+      sequences_.push_back({run_starts[k], run_starts[k + 1] - run_starts[k], positions_h_[run_starts[k]]});
+    // Every request's visible prefix (positions up to its last row) must have
+    // slots, none of them the output slot of another (request, position).
+    max_position_.assign(request_count, -1);
+    for (int64_t i = 0; i < m; ++i)
+      max_position_[requests_h_[i]] = std::max(max_position_[requests_h_[i]], positions_h_[i]);
+    const auto writer_of = [&](int32_t slot) -> int64_t {  // the row writing `slot`, or -1
+      const auto it = std::lower_bound(by_slot.begin(), by_slot.end(), slot,
+                                       [&](int64_t row, int32_t s) { return loc_p[row] < s; });
+      return it != by_slot.end() && loc_p[*it] == slot ? *it : -1;
+    };
     for (int64_t request = 0; request < request_count; ++request) {
+      const int32_t* row_map = mapping_h_.data() + request * context;
       for (int32_t position = 0; position <= max_position_[request]; ++position) {
-        const auto slot = mapping_h_[request * context + position];
-        TORCH_CHECK(slot >= 0, "GaudiRT: missing KV slot in a visible prefix");
-        auto target = targets.find(slot);
-        TORCH_CHECK(target == targets.end() ||
-                        (target->second.first == request && target->second.second == position),
+        TORCH_CHECK(row_map[position] >= 0, "GaudiRT: missing KV slot in a visible prefix");
+        const int64_t writer = writer_of(row_map[position]);
+        TORCH_CHECK(writer < 0 || (requests_h_[writer] == request && positions_h_[writer] == position),
                     "GaudiRT: output KV slot aliases another visible prefix position");
       }
     }
@@ -343,32 +363,32 @@ class PagedMetadata : public torch::CustomClassHolder {
                     mapping.numel() <= std::numeric_limits<int32_t>::max(),
                 "GaudiRT device metadata: dimensions outside supported range");
     const int64_t bucket = static_cast<int64_t>(std::bit_ceil(static_cast<uint64_t>(m)));
-    std::vector<int32_t> row_seq(m), seq_prefix(batch), seq_first(batch), last(batch);
-    std::vector<int64_t> seq_visible(batch);
-    positions_h_.resize(m);
-    int64_t cursor = 0, visible = 0;
+    // Sequence s owns rows [seq_first[s], seq_first[s] + lengths[s]) at positions
+    // prefixes[s] + i; seq_visible[s] counts the visible keys of the earlier
+    // sequences. Each sequence is checked as its rows are laid out, so the
+    // first bad one is reported.
+    std::vector<int32_t> seq_first(batch + 1, 0), seq_prefix(batch), last(batch), row_seq(m);
+    std::vector<int64_t> seq_visible(batch + 1, 0);
+    positions_h_.assign(m, 0);
     for (int64_t s = 0; s < batch; ++s) {
-      const int64_t prefix = prefixes[s], length = lengths[s];
-      TORCH_CHECK(prefix >= 0 && prefix < context && length > 0 && length <= context - prefix && length <= m - cursor,
+      const int64_t prefix = prefixes[s], length = lengths[s], row0 = seq_first[s];
+      TORCH_CHECK(prefix >= 0 && prefix < context && length > 0 && length <= context - prefix && length <= m - row0,
                   "GaudiRT device metadata: invalid sequence lengths");
-      sequences_.push_back({static_cast<int32_t>(cursor), static_cast<int32_t>(length), static_cast<int32_t>(prefix)});
+      seq_first[s + 1] = static_cast<int32_t>(row0 + length);
+      seq_visible[s + 1] = seq_visible[s] + prefix + length;
       seq_prefix[s] = static_cast<int32_t>(prefix);
-      seq_first[s] = static_cast<int32_t>(cursor);
-      seq_visible[s] = visible;
-      visible += prefix + length;
-      for (int64_t i = 0; i < length; ++i, ++cursor) {
-        row_seq[cursor] = static_cast<int32_t>(s);
-        positions_h_[cursor] = static_cast<int32_t>(prefix + i);
-      }
-      last[s] = static_cast<int32_t>(cursor - 1);
+      last[s] = seq_first[s + 1] - 1;
+      std::fill(row_seq.begin() + row0, row_seq.begin() + row0 + length, static_cast<int32_t>(s));
+      std::iota(positions_h_.begin() + row0, positions_h_.begin() + row0 + length, static_cast<int32_t>(prefix));
+      sequences_.push_back({static_cast<int32_t>(row0), static_cast<int32_t>(length), static_cast<int32_t>(prefix)});
     }
-    TORCH_CHECK(cursor == m, "GaudiRT device metadata: sequence lengths do not cover token rows");
-    if (positions_on_cpu) {
-      const auto* host_positions = positions.data_ptr<int64_t>();
-      for (int64_t row = 0; row < m; ++row)
-        TORCH_CHECK(host_positions[row] == positions_h_[row],
-                    "GaudiRT device metadata: host position does not match scheduler lengths");
-    }
+    TORCH_CHECK(seq_first[batch] == m, "GaudiRT device metadata: sequence lengths do not cover token rows");
+    if (positions_on_cpu)
+      TORCH_CHECK(std::equal(positions_h_.begin(), positions_h_.end(), positions.data_ptr<int64_t>()),
+                  "GaudiRT device metadata: host position does not match scheduler lengths");
+    const int64_t visible = seq_visible[batch];
+    seq_first.pop_back();
+    seq_visible.pop_back();
     // One buffer: host-staged words first (one copy), then the device outputs.
     int64_t words = 0;
     const auto header_offset = reserve_words(words, 1);
@@ -686,11 +706,13 @@ at::Tensor bucket_output(const at::Tensor& like, int64_t rows, int64_t width) {
 }
 
 // Rows of a 2-D bf16 matrix as the kernels take them: 16-byte aligned, row
-// stride a multiple of 8 elements, unit column stride; else a packed copy.
+// stride a multiple of 8 elements, unit column stride; else a packed copy in
+// fresh storage (contiguous() would hand back a contiguous view whose start is
+// not 16-byte aligned unchanged).
 at::Tensor kernel_rows(const at::Tensor& t) {
   const bool ok = t.stride(1) == 1 && t.stride(0) % 8 == 0 && t.stride(0) >= t.size(1) &&
                   (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0;
-  return ok ? t : t.contiguous();
+  return ok ? t : t.clone(at::MemoryFormat::Contiguous);
 }
 
 // paged_attn_validated / paged_attn_internal (src/bridge/paged_attention.cpp:164-347):

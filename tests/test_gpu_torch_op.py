@@ -262,3 +262,28 @@ def test_mixed_prefill_and_decode_batch(torch_ext, heads, kv_heads, dim, block):
     assert np.array_equal(bits(pool[0]), expected)
     problem = orc.Problem(bits(q_cpu), expected, req, pos, mapping, heads, kv_heads, dim, scale)
     print("mixed batch", check(bits(out), problem), flush=True)
+
+
+def test_misaligned_contiguous_views_are_packed(torch_ext):
+    """Q/K/V that are contiguous but start at an odd element (not 16-byte
+    aligned) are packed into fresh storage before the kernels read them, as the
+    reference packs unaligned inputs (src/bridge/paged_attention.cpp:230-245):
+    the result equals the aligned call bit for bit, the KV pool included."""
+    torch = torch_ext
+    aligned, meta, scale = run_case(torch, 8, 2, 128, 16, 64, 37)
+    actual, problem, out, (q, k, v, key_pool, value_pool) = aligned[0]
+
+    def odd_view(t):
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+        view = buf[1:].view(t.shape)
+        view.copy_(t)
+        assert view.is_contiguous() and view.data_ptr() % 16 != 0
+        return view
+
+    # The store is idempotent (the same rows to the same slots), so the pool the
+    # second call attends equals the first call's.
+    again = torch.ops.gaudirt.paged_attn.default(odd_view(q), odd_view(k), odd_view(v), key_pool, value_pool, meta,
+                                                 128, scale)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(again), actual)
+    assert np.array_equal(np.stack([bits(key_pool.transpose(0, 1)), bits(value_pool.transpose(0, 1))]), problem.pool)
