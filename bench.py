@@ -60,19 +60,35 @@ def parse_args():
     return ap.parse_args()
 
 
-def measured_traffic(kernel, workload):
-    """HBM bytes per launch of the dominant kernel, as last measured with rocprofv3 PMC
-    (FETCH_SIZE x2 + WRITE_SIZE) and recorded with its command in
-    profiles/<kernel>_<workload>_traffic.md; None when no measurement exists."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.md")
+# The dominant kernel of each workload, as rocprofv3 names it (template
+# arguments: head_dim, softcap, slot-lookup mode).
+DOMINANT_KERNEL = {
+    "c2": "decode_stream_kernel<128, false, 0>",
+    "c3": "decode_stream_kernel<128, false, 0>",
+    "c5": "decode_stream_kernel<128, false, 0>",
+    "c4": "prefill_kernel<128, false, 0>",
+}
+
+
+def measured_traffic(workload, root=ROOT):
+    """HBM bytes per launch of the workload's dominant kernel, as last measured with
+    rocprofv3 PMC (FETCH_SIZE x2 + WRITE_SIZE) and recorded with its command in
+    profiles/<kernel>_<workload>_traffic.md. None when no measurement exists, or when
+    the file measured another kernel than the one this build launches (its
+    `kernel:` line must name DOMINANT_KERNEL[workload])."""
+    kernel = DOMINANT_KERNEL[workload]
+    path = os.path.join(root, "profiles", f"{kernel.split('<')[0]}_{workload}_traffic.md")
+    recorded, traffic = None, None
     try:
         with open(path) as fh:
             for line in fh:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
+                if line.startswith("kernel:"):
+                    recorded = line.split(":", 1)[1].strip()
+                elif line.startswith("traffic_bytes_per_launch:"):
+                    traffic = int(line.split(":", 1)[1])
     except OSError:
-        pass
-    return None
+        return None
+    return traffic if recorded == kernel else None
 
 
 def cpu_baseline(dc, target_seconds):
@@ -81,7 +97,7 @@ def cpu_baseline(dc, target_seconds):
 
     from oracle import oracle as orc
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = orc.host_threads()
     query, pool = dc.host_arrays()
     context = int(dc.lens.max())
     mapping = orc.mapping_from_block_table(dc.tables, dc.block_size, context)
@@ -125,7 +141,13 @@ def host_cpu():
                     break
     except OSError:
         pass
-    return f"{model} ({os.cpu_count()} logical CPUs visible)"
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return (f"{model} ({os.cpu_count()} logical CPUs, {usable} in this process's affinity mask"
+            + (f", OMP_NUM_THREADS={omp}" if omp else "") + ")")
 
 
 def prefill_bench(args):
@@ -167,7 +189,7 @@ def prefill_bench(args):
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic", "config": {"workload": f"c4: {WORKLOADS['c4']}", "flops_per_step": pc.flops()},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": measured_traffic("prefill", "c4")},
+                     "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": measured_traffic("c4")},
         "cpu_baseline": None}), flush=True)
 
 
@@ -283,7 +305,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": measured_traffic("decode_stream", args.workload),
+            "traffic": measured_traffic(args.workload),
         },
         "cpu_baseline": cpu,
     }

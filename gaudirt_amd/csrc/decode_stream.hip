@@ -362,12 +362,12 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
-      lds_dma16(kl + i * 1024, krs, row_of(t, keyed, i, tt) + ((pc ^ swz(tt, D / 8)) << 4));
+      lds_dma16_once(kl + i * 1024, krs, row_of(t, keyed, i, tt) + ((pc ^ swz(tt, D / 8)) << 4));
     }
 #pragma unroll
     for (int i = 0; i < S::LOADS; ++i) {
       const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
-      lds_dma16(vl + i * 1024, vrs, row_of(t, keyed, i, tt) + ((pc ^ swz(tt, D / 8)) << 4));
+      lds_dma16_once(vl + i * 1024, vrs, row_of(t, keyed, i, tt) + ((pc ^ swz(tt, D / 8)) << 4));
     }
   };
   // The unit's query heads -> LDS ([head][D], row-major). The resource covers

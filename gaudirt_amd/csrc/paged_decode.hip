@@ -13,10 +13,10 @@
 //    Scores are computed transposed, S^T[token][head] = K . Q^T with
 //    v_mfma_f32_16x16x32_bf16, which leaves each lane holding one head's
 //    scores for 8 tokens: exactly the A operand of the P.V MFMA, so
-//    probabilities never move between lanes. K goes from HBM straight into
-//    MFMA operand registers with 16-byte buffer loads. V is loaded the same
-//    way, written to LDS row-major with its 16-byte chunks XOR-swizzled by
-//    token, and read back transposed with ds_read_b64_tr_b16 as the B operand
+//    probabilities never move between lanes. K and V tiles go HBM -> LDS with
+//    16-byte buffer->LDS loads (two stages), rows stored with their 16-byte
+//    chunks XOR-swizzled by token; K is read back with ds_read_b128 as the A
+//    operand of S^T, V transposed with ds_read_b64_tr_b16 as the B operand
 //    [token][dim] of P.V.
 //
 //  * decode_dot_kernel (groups 1..3, where a 16-row MFMA tile would be mostly
@@ -164,13 +164,15 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
       for (int i = 0; i < S::LOADS; ++i) {
         const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + i * 1024), 16,
-                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4), 0, 0, 0);
+                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4), 0, 0,
+                                                 kKvLoadPolicyBits);
       }
 #pragma unroll
       for (int i = 0; i < S::LOADS; ++i) {
         const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + i * 1024), 16,
-                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4), 0, 0, 0);
+                                                 row0 + tt * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4), 0, 0,
+                                                 kKvLoadPolicyBits);
       }
     } else {
 #pragma unroll
@@ -178,14 +180,14 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
         const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
         const uint32_t row = (uint32_t)slot_of(s_bt, b0, shift, min(tb + tt, t_last)) * (2 * D);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(kt + i * 1024), 16, row + ((pc ^ swz(tt, D / 8)) << 4),
-                                                 0, 0, 0);
+                                                 0, 0, kKvLoadPolicyBits);
       }
 #pragma unroll
       for (int i = 0; i < S::LOADS; ++i) {
         const int s = i * 64 + lane, tt = s / S::CPR, pc = s % S::CPR;
         const uint32_t row = (uint32_t)slot_of(s_bt, b0, shift, min(tb + tt, t_last)) * (2 * D);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(vt + i * 1024), 16, row + ((pc ^ swz(tt, D / 8)) << 4),
-                                                 0, 0, 0);
+                                                 0, 0, kKvLoadPolicyBits);
       }
     }
   };
@@ -428,10 +430,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_dot_kernel(DecodeArgs a) {
       // Keys past the partition read its last key (mapped, in bounds); masked below.
       const int slot = slot_of(s_bt, b0, shift, min(t, pr.t_end - 1));
       const uint16_t* kp = kbase + (int64_t)slot * D;
-      ka[u] = load16(kp + c0);
-      kb[u] = load16(kp + c1);
-      va[u] = load16(kp + vhalf + c0);
-      vb[u] = load16(kp + vhalf + c1);
+      ka[u] = load16_once(kp + c0);
+      kb[u] = load16_once(kp + c1);
+      va[u] = load16_once(kp + vhalf + c0);
+      vb[u] = load16_once(kp + vhalf + c1);
     }
 
     float p[U][G];

@@ -15,26 +15,42 @@ def recorded(name):
         return int(re.search(r"^traffic_bytes_per_launch: (\d+)$", fh.read(), re.M).group(1))
 
 
-def test_traffic_records_are_read_from_profiles():
-    assert bench.measured_traffic("decode_stream", "c2") == recorded("decode_stream_c2_traffic.md")
-    assert bench.measured_traffic("prefill", "c4") == recorded("prefill_c4_traffic.md")
-    assert bench.measured_traffic("decode_stream", "c5") is None  # no record: null, not a guess
+def test_traffic_records_name_the_shipping_kernel(tmp_path):
+    # A record counts only when its kernel line names the kernel this build launches.
+    (tmp_path / "profiles").mkdir()
+    good = tmp_path / "profiles" / "decode_stream_kernel_c2_traffic.md"
+    good.write_text(f"kernel: {bench.DOMINANT_KERNEL['c2']}\ntraffic_bytes_per_launch: 123\n")
+    assert bench.measured_traffic("c2", root=str(tmp_path)) == 123
+    good.write_text("kernel: decode_stream_kernel<128, false, false>\ntraffic_bytes_per_launch: 123\n")
+    assert bench.measured_traffic("c2", root=str(tmp_path)) is None  # an older template: stale
+    assert bench.measured_traffic("c5", root=str(tmp_path)) is None  # no record: null, not a guess
+    for workload in ("c2", "c3", "c4", "c5"):
+        value = bench.measured_traffic(workload)
+        kernel = bench.DOMINANT_KERNEL[workload]
+        path = os.path.join(ROOT, "profiles", f"{kernel.split('<')[0]}_{workload}_traffic.md")
+        if value is not None:
+            assert value == recorded(os.path.basename(path))
 
 
 def test_traffic_records_match_their_counters():
-    # FETCH_SIZE (KiB, reported at half the bytes read) x 2 + WRITE_SIZE (KiB) x 1.
-    for name, kernel in [("decode_stream_c2_traffic.md", "decode_stream_kernel"),
-                         ("prefill_c4_traffic.md", "prefill_kernel")]:
+    # FETCH_SIZE (KiB, reported at half the bytes read) x 2 + WRITE_SIZE (KiB) x 1, for the
+    # kernel the record names.
+    for name in sorted(os.listdir(os.path.join(ROOT, "profiles"))):
+        if not name.endswith("_traffic.md"):
+            continue
         with open(os.path.join(ROOT, "profiles", name)) as fh:
             text = fh.read()
-        row = re.search(r"^\| " + kernel + r"<[^|]*> \| (\d+) \| (\d+) \|$", text, re.M)
+        kernel = re.search(r"^kernel: (.*)$", text, re.M)
+        if kernel is None:
+            continue
+        row = re.search(r"^\| " + re.escape(kernel.group(1)) + r" \| (\d+) \| (\d+) \|$", text, re.M)
         fetch, write = int(row.group(1)), int(row.group(2))
-        assert recorded(name) == (2 * fetch + write) * 1024
+        assert recorded(name) == (2 * fetch + write) * 1024, name
 
 
 def test_host_cpu_description():
     text = bench.host_cpu()
-    assert "logical CPUs visible" in text and str(os.cpu_count()) in text
+    assert "logical CPUs" in text and "affinity mask" in text and str(os.cpu_count()) in text
 
 
 def test_more_than_one_gpu_is_refused():
