@@ -20,11 +20,13 @@ GK_ERR_UNSUPPORTED = 2
 GK_ERR_HIP = 3
 GK_ERR_OUT_OF_MEMORY = 4
 GK_ERR_WORKSPACE = 5
+GK_DECODE_SCRATCH_BYTES = 32 << 20
 
 # Every function include/gaudirt_amd.h declares.
 EXPORTED = [
     "gk_last_error", "gk_version", "gk_kv_store", "gk_paged_decode_workspace_bytes",
-    "gk_paged_decode_partition_tokens", "gk_paged_decode", "gk_paged_prefill", "gk_split_k_merge",
+    "gk_paged_decode_partition_tokens", "gk_paged_decode", "gk_paged_decode_scratch", "gk_paged_prefill",
+    "gk_split_k_merge",
     "gk_attn_tile_indices", "gk_advance_decode_lengths",
     "gk_metadata_workspace_bytes", "gk_metadata_normalize", "gk_block_tables",
     "gk_paged_alloc_slots", "gk_paged_release_workspace_bytes", "gk_paged_release_slots",
@@ -145,6 +147,7 @@ def load():
     lib.gk_paged_decode_partition_tokens.restype = c_i32
     lib.gk_paged_decode_partition_tokens.argtypes = [ctypes.POINTER(DecodeParams)]
     lib.gk_paged_decode.argtypes = [ctypes.POINTER(DecodeParams), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.gk_paged_decode_scratch.argtypes = [ctypes.POINTER(DecodeParams), c_void_p]
     lib.gk_paged_prefill.argtypes = [ctypes.POINTER(PrefillParams), c_void_p]
     lib.gk_kv_store.argtypes = [c_void_p, c_void_p, c_i64, c_i64, c_void_p, c_i32, c_void_p, c_i64, c_i32, c_i32,
                                 c_void_p]

@@ -38,6 +38,7 @@
 #include "decode_common.hpp"
 
 #include <algorithm>
+#include <mutex>
 
 namespace gk {
 namespace {
@@ -890,6 +891,59 @@ int split_k_merge(const float* partial_out, const float* partial_ml, const int32
   return hip_status(hipGetLastError(), "gk_split_k_merge launch");
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split-K workspace in a static device array
+// ---------------------------------------------------------------------------
+namespace {
+
+// Every GPU the library runs on holds this array until the process ends. Each
+// device has its own copy at its own address, looked up once per device with
+// hipGetSymbolAddress; host code uses only that address, never the name.
+static __device__ __align__(256) unsigned char scratch[GK_DECODE_SCRATCH_BYTES];
+
+std::mutex scratch_mutex;
+void* scratch_address[64] = {};
+
+// Address of `scratch` on the current device (which must be the stream's).
+int scratch_on_device(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (int rc = hip_status(hipGetDevice(&dev), "gk_paged_decode_scratch: hipGetDevice")) return rc;
+  hipDevice_t stream_dev = dev;
+  if (int rc = hip_status(hipStreamGetDevice(stream, &stream_dev), "gk_paged_decode_scratch: hipStreamGetDevice"))
+    return rc;
+  if (stream_dev != dev)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_decode_scratch: the stream belongs to another device than the current one");
+  if (dev < 0 || dev >= 64) return fail(GK_ERR_UNSUPPORTED, "gk_paged_decode_scratch: device index above 63");
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_address[dev]) {
+    void* address = nullptr;
+    if (int rc = hip_status(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)),
+                            "gk_paged_decode_scratch: hipGetSymbolAddress"))
+      return rc;
+    scratch_address[dev] = address;
+  }
+  *out = scratch_address[dev];
+  return GK_OK;
+}
+
+}  // namespace
+
+// Nothing in the workspace has to start at zero: every partial and every span
+// record the merge reads is written by the same call's decode kernel first.
+int paged_decode_scratch(const gk_decode_params* p, hipStream_t stream) {
+  if (int rc = validate(p)) return rc;
+  if (p->rows == 0) return GK_OK;
+  const size_t need = decode_workspace_bytes(p);
+  if (need > GK_DECODE_SCRATCH_BYTES)
+    return fail(GK_ERR_WORKSPACE, "gk_paged_decode_scratch: these parameters need " + std::to_string(need) +
+                                      " bytes of workspace, more than the " + std::to_string(GK_DECODE_SCRATCH_BYTES) +
+                                      "-byte static scratch; call gk_paged_decode with a workspace instead");
+  void* workspace = nullptr;
+  if (need)
+    if (int rc = scratch_on_device(stream, &workspace)) return rc;
+  return paged_decode(p, workspace, need, stream);
+}
+
 }  // namespace gk
 
 extern "C" size_t gk_paged_decode_workspace_bytes(const gk_decode_params* params) {
@@ -912,4 +966,9 @@ extern "C" int gk_split_k_merge(const float* partial_out, const float* partial_m
   gk::clear_error();
   return gk::split_k_merge(partial_out, partial_ml, part_count, rows, heads, max_parts, head_dim, out,
                            out_row_stride, stream);
+}
+
+extern "C" int gk_paged_decode_scratch(const gk_decode_params* params, hipStream_t stream) {
+  gk::clear_error();
+  return gk::paged_decode_scratch(params, stream);
 }

@@ -112,6 +112,21 @@ int32_t gk_paged_decode_partition_tokens(const gk_decode_params* params);
 int gk_paged_decode(const gk_decode_params* params, void* workspace, size_t workspace_bytes,
                     hipStream_t stream);
 
+/* Allocation-free gk_paged_decode. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same parameters,
+ * kernels and results as gk_paged_decode, whose workspace here is a static
+ * device array of GK_DECODE_SCRATCH_BYTES that every GPU the library runs on
+ * holds until the process ends (located on the first call on each device;
+ * the current device must be the stream's). Parameters whose workspace
+ * (gk_paged_decode_workspace_bytes) exceeds it are rejected with
+ * GK_ERR_WORKSPACE before anything is enqueued. All calls on one GPU share the
+ * array: calls that overlap on one GPU (on different streams, or from
+ * different threads) race and must be serialised by the caller; calls on one
+ * stream are ordered by it. */
+#define GK_DECODE_SCRATCH_BYTES (32u << 20)
+int gk_paged_decode_scratch(const gk_decode_params* params, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Chunked / prefix-shared prefill attention with bf16 MFMA. Replaces the
  * prefill blocks of src/bridge/paged_attention.cpp:264-345 (query blocks of up
