@@ -6,15 +6,15 @@
 // The chunk's own K/V rows are already in the pool (the store runs first), so
 // every key is read through the block table.
 //
-// Work decomposition. A workgroup of four waves owns one (sequence, kv head,
-// tile of rows). The GQA group is folded into the tile: its 128 "query rows"
+// Work decomposition. A workgroup of eight waves owns one (sequence, kv head,
+// tile of rows). The GQA group is folded into the tile: its 256 "query rows"
 // are (row, head) pairs, so one K/V tile serves every head of the group. Each
-// wave computes 32 query rows (two 16-column MFMA tiles) against 32 keys per
-// step:
+// wave computes 32 query rows (two 16-column MFMA tiles) against the keys of
+// a step (64 at head_dim 128, 32 at head_dim 64):
 //   S^T[key][qrow] = K . Q^T      v_mfma_f32_16x16x32_bf16, K from LDS
 //   O[qrow][dim]  += P . V        P straight from S^T's registers, V read
 //                                 transposed from LDS (ds_read_b64_tr_b16)
-// K and V tiles of 32 keys are shared by the four waves through LDS: 16-byte
+// A step's K and V tiles are shared by the eight waves through LDS: 16-byte
 // buffer->LDS loads issued by the whole workgroup, XOR-swizzled by token,
 // double-buffered so the next tile streams in while the current one is used.
 // Online softmax runs in log2 units with a lazily re-based running maximum.
@@ -31,21 +31,30 @@
 namespace gk {
 namespace {
 
-// Waves per workgroup (each owns 16 * kNT query rows). Eight waves (half the
-// K/V re-reads) measured 2% slower on C4 than four.
-constexpr int kPrefillWaves = 4;
-// 16-column query tiles per wave. Two, with two workgroups per CU: three or
-// four tiles per wave (one workgroup per CU) measured 2x slower on C4, the
-// barrier waits no longer hidden by a second workgroup.
+// Waves per workgroup (each owns 16 * kNT query rows). Eight, one workgroup
+// per CU (two waves per SIMD): each K/V tile is loaded into LDS once for 256
+// query rows instead of twice for two 128-row workgroups (C4, 64-key steps,
+// same box: 180.0 -> 174.1 us with four -> eight waves; 168.8 us together with
+// the early V reads below).
+constexpr int kPrefillWaves = 8;
+// 16-column query tiles per wave. Two: three fit in 256 VGPRs only without the
+// early V reads, and four spill; both also quantise C4's rows badly (48- or
+// 64-row tiles of 512-row chunks leave a partial round of workgroups).
 constexpr int kNT = 2;
 constexpr int kQrowsPerWave = 16 * kNT;
 constexpr int kQrows = kPrefillWaves * kQrowsPerWave;     // query rows per workgroup
-constexpr int kKeys = 32;                                  // keys per step
+// Keys per step: 64 at head_dim 128 (half the per-step barriers, cross-lane
+// maxima, re-base checks and load setup of 32-key steps: C4 178.1 -> 166.8
+// us); 32 at head_dim 64, whose 64-key form needs 130 VGPRs and so would drop
+// from four waves per SIMD to three.
+template <int D>
+constexpr int prefill_keys() { return D >= 128 ? 64 : 32; }
 // K/V pipeline depth. Two: three and four stages measured the same on C4 (the
 // kernel is bound by its instruction stream, not by load latency).
 constexpr int kStages = 2;
-static_assert(kStages >= 2 && kStages <= 4, "wait counts cover up to two stages in flight");
 constexpr float kLazyRescale = 8.f;
+// XCDs of an MI355X: consecutive workgroups of a launch go to consecutive XCDs.
+constexpr int kXcds = 8;
 
 struct PrefillArgs {
   const uint16_t* query;
@@ -73,12 +82,12 @@ struct PrefillShape {
   static constexpr int NC = D / 32;                 // 32-dim k chunks of Q.K
   static constexpr int CPR = D / 8;                 // 16-byte chunks per head row
   static constexpr int NO = D / 16;                 // 16-dim output chunks
-  static constexpr int TILE = kKeys * D * 2;        // bytes of one K or V tile
+  static constexpr int TILE = prefill_keys<D>() * D * 2;  // bytes of one K or V tile
   static constexpr int NI = TILE / 1024;            // 1 KiB load instructions per tile
 };
 
 // How a step's slots are found (the MODE template argument):
-//  kStepBlocks  blocks of >= 32 keys: one scalar block-table entry per step;
+//  kStepBlocks  blocks of at least a step's keys: one scalar block-table entry per step;
 //  kLoadBlocks  blocks of >= 64 / (D / 8) keys (one load instruction's): one
 //               scalar entry per load instruction;
 //  kKeyBlocks   shorter blocks, down to the token-granular map (block 1): each
@@ -86,9 +95,14 @@ struct PrefillShape {
 constexpr int kStepBlocks = 0, kLoadBlocks = 1, kKeyBlocks = 2;
 
 template <int D, bool SOFTCAP, int MODE>
-__global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
   using S = PrefillShape<D>;
-  constexpr int LPW = S::NI / kPrefillWaves;         // load instructions per wave per K (or V) tile
+  constexpr int kKeys = prefill_keys<D>();
+  static_assert(kKeys == 32 || kKeys == 64, "a step is one or two 32-key halves");
+  constexpr int kKG = kKeys / 16;  // 16-key groups per step (Q.K tiles)
+  constexpr int kKH = kKeys / 32;  // 32-key halves per step (P.V k chunks)
+  // Load instructions per wave per K (or V) tile; wave w issues instructions w, w + waves, ...
+  constexpr int LPW = (S::NI + kPrefillWaves - 1) / kPrefillWaves;
   constexpr int NE = MODE == kStepBlocks ? 1 : LPW;  // block-table entries per wave (per lane) per step
   constexpr int KPL = kKeys / S::NI;                 // keys of one load instruction
   constexpr bool CLAMPED = MODE != kStepBlocks;      // entries of keys outside [key_begin, key_end) clamped
@@ -101,9 +115,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS bases of the direct loads)
   const int q = lane >> 4, c16 = lane & 15;
-  // Work item (row tile, kv head, sequence), row tiles fastest.
-  const int item = blockIdx.x;
-  const int tile = item % a.tiles, kvh = (item / a.tiles) % a.kv_heads, seq = item / (a.tiles * a.kv_heads);
+  // Work item (row tile, sequence, kv head), row tiles fastest, kv heads
+  // slowest. Workgroup b runs on XCD b % 8, so b is mapped to items with each
+  // XCD taking one contiguous eighth of that order: the workgroups sharing a
+  // kv head's K/V (every row tile of every sequence, which share the prefix)
+  // run under one L2 instead of fetching it into all eight.
+  const int nitems = gridDim.x, xcd = blockIdx.x % kXcds, per_xcd = nitems / kXcds, extra = nitems % kXcds;
+  const int item = xcd * per_xcd + min(xcd, extra) + (int)blockIdx.x / kXcds;
+  const int tile = item % a.tiles, seq = (item / a.tiles) % a.seqs, kvh = item / (a.tiles * a.seqs);
   const int rows = a.seq_rows[seq];
   const int r0 = tile * a.rows_per_tile;
   if (r0 >= rows) return;
@@ -143,14 +162,15 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   const int wave_left_max =
       a.window > 0 ? pos_lo + min(nr - 1, (wave * kQrowsPerWave + kQrowsPerWave - 1) / g) - a.window + 1 : 0;
 
-  // At d 128 the V operands are read before the softmax (their LDS latency
-  // behind its arithmetic) and the row sums of the bf16 probabilities run on
+  // At d 128 the V operands of the step's first 32 keys are read before the
+  // softmax (their LDS latency behind its arithmetic; all 64 keys' would not
+  // fit the registers) and the row sums of the bf16 probabilities run on
   // one more MFMA per step against an all-ones operand, in the output layout
   // (rows 4q + r). At d 64 the registers these take would drop the kernel
   // from four waves per SIMD to three, which costs more than they save: V is
   // read next to its MFMAs and each lane sums its query row on the VALU
   // (component 0 of l_run).
-  constexpr bool kEarlyV = D >= 128;
+  constexpr bool kEarlyV = D >= 128;  // the first 32-key half's V operands (32 VGPRs)
   constexpr bool kMfmaSum = D >= 128;
   f32x4_t o[kNT][S::NO];
   float m_run[kNT];
@@ -170,8 +190,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, region, kBufferDword3);
   const int shift = a.block_shift, bmask = (1 << shift) - 1;
 
-  // Direct loads of the 32-key step at tb into one stage. Steps are 32-aligned.
-  // Blocks of >= 32 keys hold a whole step: its slots are consecutive from the
+  // Direct loads of the step at tb into one stage. Steps are kKeys-aligned.
+  // Blocks of >= kKeys keys hold a whole step: its slots are consecutive from the
   // block's slot for tb (one scalar block-table read). Blocks of >= KPL keys
   // hold whole load instructions: each of this wave's loads reads its own
   // entry. Shorter blocks: each lane reads the entry of its own key.
@@ -189,6 +209,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
 #pragma unroll
     for (int k = 0; k < LPW; ++k) {
       const int ins = wave + k * kPrefillWaves;
+      if (S::NI % kPrefillWaves != 0 && ins >= S::NI) break;  // wave-uniform
       const int p = ins * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
       uint32_t row;  // byte offset of the lane's key row
       if constexpr (MODE == kKeyBlocks) {
@@ -236,9 +257,9 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       __syncthreads();
     }
     // S^T = K.Q^T: lane (q, c16) gets qrow c16 (+16 nt), keys tb + 16h + 4q + r.
-    f32x4_t sc[2][kNT];
+    f32x4_t sc[kKG][kNT];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kKG; ++h) {
       const int tt = 16 * h + c16;
       bf16x8_t kr[S::NC];
 #pragma unroll
@@ -252,11 +273,11 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       }
     }
 
-    // V operand c of P . V: keys 4q + (c16 >> 2) and 16 + 4q + (c16 >> 2),
-    // dims 16c + 4 (c16 & 3), read transposed.
-    auto read_v = [&](int c) {
+    // V operand c of P . V for the 32-key half hh: keys 32hh + 4q + (c16 >> 2)
+    // and 32hh + 16 + 4q + (c16 >> 2), dims 16c + 4 (c16 & 3), read transposed.
+    auto read_v = [&](int hh, int c) {
       const int lc = 2 * c + ((c16 & 3) >> 1);
-      const int t0 = 4 * q + (c16 >> 2), t1 = t0 + 16;
+      const int t0 = 32 * hh + 4 * q + (c16 >> 2), t1 = t0 + 16;
       const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3));
       const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3));
       return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -264,7 +285,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
     bf16x8_t vb[kEarlyV ? S::NO : 1];
     if constexpr (kEarlyV) {
 #pragma unroll
-      for (int c = 0; c < S::NO; ++c) vb[c] = read_v(c);
+      for (int c = 0; c < S::NO; ++c) vb[c] = read_v(0, c);
     }
 
     // A step whose keys every valid query row of this wave sees (below the
@@ -273,13 +294,13 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
     // place (the same registers on both paths), the row maximum is taken on raw
     // scores (scale > 0), and p = exp2(fma(s, scale, -max)).
     const bool full = !SOFTCAP && tb + kKeys - 1 <= wave_pos_min && tb >= wave_left_max;
-    bf16x8_t pa[kNT];
+    bf16x8_t pa[kKH][kNT];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
       float mx = -INFINITY;
       if constexpr (SOFTCAP) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < kKG; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int key = tb + 16 * h + 4 * q + r;
@@ -291,7 +312,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
       } else {
         if (!full) {
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
+          for (int h = 0; h < kKG; ++h)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int key = tb + 16 * h + 4 * q + r;
@@ -299,11 +320,34 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
             }
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < kKG; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[h][nt][r]);
         mx *= a.score_scale;
       }
+      // The probabilities are formed right away against the running maximum;
+      // the step's maximum is reduced across lanes alongside them and only
+      // decides afterwards whether the (rare) re-base is due, which then
+      // recomputes them against the new maximum. Same values as re-basing
+      // first; the exponentials no longer wait for the cross-lane reduction.
+      auto probabilities = [&](float base) {
+        float ps[4 * kKG];
+#pragma unroll
+        for (int i = 0; i < 4 * kKG; ++i) {
+          if constexpr (SOFTCAP) ps[i] = fast_exp2(sc[i >> 2][nt][i & 3] - base);
+          else ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
+        }
+#pragma unroll
+        for (int i = 0; i < 4 * kKG; ++i) pa[i >> 3][nt][i & 7] = (__bf16)ps[i];
+        if constexpr (!kMfmaSum) {
+          float l = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4 * kKG; ++i) l += ps[i];
+          return l;
+        }
+        return 0.f;
+      };
+      float lsum = probabilities(m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
       mx = col4_max(mx);
       if (__builtin_amdgcn_ballot_w64(mx > m_run[nt] + kLazyRescale)) {
         const float m_new = fmaxf(m_run[nt], mx);
@@ -318,66 +362,59 @@ __global__ __launch_bounds__(kPrefillWaves * 64, kNT >= 3 ? 1 : 2) void prefill_
           for (int c = 0; c < S::NO; ++c) o[nt][c][r] *= f;
           if constexpr (kMfmaSum) l_run[nt][r] *= f;
         }
+        lsum = probabilities(m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
       }
-      const float base = m_run[nt] == -INFINITY ? 0.f : m_run[nt];
-      float ps[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if constexpr (SOFTCAP) ps[i] = fast_exp2(sc[i >> 2][nt][i & 3] - base);
-        else ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if constexpr (!kMfmaSum) l_run[nt][0] += ps[i];
-        pa[nt][i] = (__bf16)ps[i];
-      }
+      if constexpr (!kMfmaSum) l_run[nt][0] += lsum;
     }
 
     // O[qrow][dim] += P . V, and the row sums.
 #pragma unroll
     for (int c = 0; c < S::NO; ++c) {
-      const bf16x8_t v = kEarlyV ? vb[kEarlyV ? c : 0] : read_v(c);
 #pragma unroll
-      for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[nt], v, o[nt][c]);
+      for (int hh = 0; hh < kKH; ++hh) {
+        const bf16x8_t v = (kEarlyV && hh == 0) ? vb[kEarlyV ? c : 0] : read_v(hh, c);
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[hh][nt], v, o[nt][c]);
+      }
     }
     if constexpr (kMfmaSum) {
       const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
                              (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
 #pragma unroll
-      for (int nt = 0; nt < kNT; ++nt) l_run[nt] = mfma32(pa[nt], ones, l_run[nt]);
+      for (int hh = 0; hh < kKH; ++hh)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) l_run[nt] = mfma32(pa[hh][nt], ones, l_run[nt]);
     }
   };
 
-  // kStages-deep pipeline over the workgroup, one barrier per step: before it
-  // each wave waits for its own loads of the current stage (the younger ones,
-  // of the next kStages - 2 stages, stay in flight); after it every wave's
-  // loads of the stage have landed and every wave has finished the previous
-  // step, whose buffer is refilled with the step kStages - 1 ahead.
-  constexpr int LPS = 2 * S::NI / kPrefillWaves;  // direct loads per wave per stage
-  static_assert(S::NI % kPrefillWaves == 0, "tile pieces split evenly over the waves");
+  // Two-stage pipeline over the workgroup, one barrier per step: before it
+  // each wave waits for its own loads of the current stage; after it every
+  // wave's loads of the stage have landed and every wave has finished the
+  // previous step, whose buffer is refilled with the next step. (Unrolling the
+  // loop over the two stages, so that each stage's LDS addresses become
+  // immediate offsets, saved address arithmetic but made the register
+  // allocator copy the accumulators on the lazy re-base branch's common edge:
+  // 183.3 against 182.5 us on C4.)
+  static_assert(kStages == 2, "the step loop alternates two stages");
   Entries e_next{};
-#pragma unroll
-  for (int st = 0; st < kStages - 1; ++st) {
-    if (st < nsteps) issue(kb0 + st * kKeys, entry_of(kb0 + st * kKeys), kv[st][0], kv[st][1]);
-  }
-  if (kStages - 1 < nsteps) e_next = entry_of(kb0 + (kStages - 1) * kKeys);
+  issue(kb0, entry_of(kb0), kv[0][0], kv[0][1]);
+  if (1 < nsteps) e_next = entry_of(kb0 + kKeys);
   for (int step = 0; step < nsteps; ++step) {
-    const int later = min(kStages - 2, nsteps - 1 - step);  // stages in flight beyond this one
-    if (later >= 2) wait_vmem<2 * LPS>();
-    else if (later == 1) wait_vmem<LPS>();
-    else wait_vmem<0>();
+    wait_vmem<0>();
     __syncthreads();
-    // Every load of this wave has landed; with per-lane entries (the only
-    // compiler-visible loads in the loop) tell the compiler, so that it adds no
-    // wait of its own after this step's direct loads.
-    if constexpr (MODE == kKeyBlocks) wait_vmem_visible();
-    const int ahead = step + kStages - 1;
-    if (ahead < nsteps) {
-      const int buf = ahead % kStages;
-      issue(kb0 + ahead * kKeys, e_next, kv[buf][0], kv[buf][1]);
-      if (ahead + 1 < nsteps) e_next = entry_of(kb0 + (ahead + 1) * kKeys);
+    // Every load of this wave has landed; tell the compiler. Its wait-count
+    // model does not see the asm direct loads or waits, so it still counts the
+    // query loads before the loop (and, with per-lane entries, the entry loads)
+    // as outstanding, and would put an s_waitcnt vmcnt(0) before their first
+    // use in the step: after this step's direct loads, which it would then
+    // wait for (C4: 185.2 -> 183.9 us).
+    wait_vmem_visible();
+    if (step + 1 < nsteps) {
+      const int next = (step + 1) & 1;
+      issue(kb0 + (step + 1) * kKeys, e_next, kv[next][0], kv[next][1]);
+      if (step + 2 < nsteps) e_next = entry_of(kb0 + (step + 2) * kKeys);
     }
-    const int cur = step % kStages;
+    const int cur = step & 1;
     consume(kb0 + step * kKeys, kv[cur][0], kv[cur][1]);
   }
 
@@ -410,8 +447,9 @@ void launch_mode(const PrefillArgs& a, bool softcap, dim3 grid, hipStream_t stre
 
 template <int D>
 void launch(const PrefillArgs& a, bool softcap, int block_size, dim3 grid, hipStream_t stream) {
-  if (block_size >= kKeys) launch_mode<D, kStepBlocks>(a, softcap, grid, stream);
-  else if (block_size >= kKeys / PrefillShape<D>::NI) launch_mode<D, kLoadBlocks>(a, softcap, grid, stream);
+  constexpr int keys = prefill_keys<D>();
+  if (block_size >= keys) launch_mode<D, kStepBlocks>(a, softcap, grid, stream);
+  else if (block_size >= keys / PrefillShape<D>::NI) launch_mode<D, kLoadBlocks>(a, softcap, grid, stream);
   else launch_mode<D, kKeyBlocks>(a, softcap, grid, stream);
 }
 
@@ -423,7 +461,7 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: struct_size does not match this library's gk_prefill_params");
   if (p->head_dim != 64 && p->head_dim != 128)
     return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: head dimension must be 64 or 128");
-  if (p->q_heads <= 0 || p->kv_heads <= 0 || p->q_heads % p->kv_heads || p->q_heads / p->kv_heads > kQrows)
+  if (p->q_heads <= 0 || p->kv_heads <= 0 || p->q_heads % p->kv_heads || p->q_heads / p->kv_heads > 128)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: invalid head geometry (GQA group at most 128)");
   if (!is_pow2(p->block_size) || p->block_size > (1 << 20))
     return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: block_size must be a power of two of at most 2^20");
