@@ -25,6 +25,7 @@
 // fp32 accumulation, one normalisation at the end by the sum of those bf16
 // probabilities, bf16 output.
 #include "gk_mfma.hpp"
+#include "work_order.hpp"
 
 #include <algorithm>
 
@@ -119,9 +120,11 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // slowest. Workgroup b runs on XCD b % 8, so b is mapped to items with each
   // XCD taking one contiguous eighth of that order: the workgroups sharing a
   // kv head's K/V (every row tile of every sequence, which share the prefix)
-  // run under one L2 instead of fetching it into all eight.
+  // run under one L2 instead of fetching it into all eight. Inside its share
+  // an XCD takes the row tiles highest first (heavy_first_item).
   const int nitems = gridDim.x, xcd = blockIdx.x % kXcds, per_xcd = nitems / kXcds, extra = nitems % kXcds;
-  const int item = xcd * per_xcd + min(xcd, extra) + (int)blockIdx.x / kXcds;
+  const int item = heavy_first_item(xcd * per_xcd + min(xcd, extra), per_xcd + (xcd < extra), a.tiles,
+                                    (int)blockIdx.x / kXcds);
   const int tile = item % a.tiles, seq = (item / a.tiles) % a.seqs, kvh = item / (a.tiles * a.seqs);
   const int rows = a.seq_rows[seq];
   const int r0 = tile * a.rows_per_tile;
