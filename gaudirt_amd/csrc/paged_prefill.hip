@@ -165,16 +165,17 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   const int wave_left_max =
       a.window > 0 ? pos_lo + min(nr - 1, (wave * kQrowsPerWave + kQrowsPerWave - 1) / g) - a.window + 1 : 0;
 
-  // At d 128 the V operands of the step's first 32 keys are read before the
-  // softmax (their LDS latency behind its arithmetic; all 64 keys' would not
-  // fit the registers) and the row sums of the bf16 probabilities run on
-  // one more MFMA per step against an all-ones operand, in the output layout
-  // (rows 4q + r). At d 64 the registers these take would drop the kernel
-  // from four waves per SIMD to three, which costs more than they save: V is
-  // read next to its MFMAs and each lane sums its query row on the VALU
-  // (component 0 of l_run).
-  constexpr bool kEarlyV = D >= 128;  // the first 32-key half's V operands (32 VGPRs)
+  // At d 128 the row sums of the bf16 probabilities run on one more MFMA per
+  // half step against an all-ones operand, in the output layout (rows 4q + r).
+  // At d 64 the registers would drop the kernel from four waves per SIMD to
+  // three, which costs more than it saves: each lane sums its query row on the
+  // VALU (component 0 of l_run).
   constexpr bool kMfmaSum = D >= 128;
+  // Step loop (below): at d 64 two groups of waves alternate between MFMA and
+  // softmax phases (C4 shapes: 113.7 -> 104.8 us); at d 128 the same order
+  // measured 158.9 -> 181.0 us, with or without the phase offset, so d 128
+  // keeps one barrier per step with every wave in Q.K -> softmax -> P.V order.
+  constexpr bool kPingPong = D < 128;
   f32x4_t o[kNT][S::NO];
   float m_run[kNT];
   f32x4_t l_run[kNT];
@@ -193,45 +194,13 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, region, kBufferDword3);
   const int shift = a.block_shift, bmask = (1 << shift) - 1;
 
-  // Direct loads of the step at tb into one stage. Steps are kKeys-aligned.
-  // Blocks of >= kKeys keys hold a whole step: its slots are consecutive from the
-  // block's slot for tb (one scalar block-table read). Blocks of >= KPL keys
-  // hold whole load instructions: each of this wave's loads reads its own
-  // entry. Shorter blocks: each lane reads the entry of its own key.
-  // Piece p = 64 ins + lane of load instruction ins (wave ins % waves): token
-  // p / CPR, stored chunk p % CPR holding the token's chunk (p % CPR) ^
-  // swz(token, D / 8).
+  // Block-table entries of the step at key tb (scalar loads, or per-lane
+  // vector loads for kKeyBlocks, fetched a step ahead: the loop's wait before
+  // its closing barrier covers them). With CLAMPED a key outside
+  // [key_begin, key_end) takes the entry of the nearest such key.
   struct Entries {
     int e[NE];
   };
-  auto issue = [&](int tb, const Entries& en, char* kt, char* vt) {
-    // Per-lane entries are vector loads of the previous step, already complete
-    // (the loop waits for every load before its barrier); say so to the compiler.
-    if constexpr (MODE == kKeyBlocks) wait_vmem_visible();
-    const uint32_t kl = lds_addr(kt), vl = lds_addr(vt);
-#pragma unroll
-    for (int k = 0; k < LPW; ++k) {
-      const int ins = wave + k * kPrefillWaves;
-      if (S::NI % kPrefillWaves != 0 && ins >= S::NI) break;  // wave-uniform
-      const int p = ins * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
-      uint32_t row;  // byte offset of the lane's key row
-      if constexpr (MODE == kKeyBlocks) {
-        row = (uint32_t)((en.e[k] << shift) | ((tb + tt) & bmask)) * (2 * D);
-      } else {
-        const int run = MODE == kLoadBlocks ? ins * KPL : 0;  // first key of the entry's run, relative to tb
-        row = (uint32_t)((en.e[MODE == kLoadBlocks ? k : 0] << shift) | ((tb + run) & bmask)) * (2 * D) +
-              (tt - run) * (2 * D);
-      }
-      const uint32_t off = row + ((pc ^ swz(tt, D / 8)) << 4);
-      lds_dma16(kl + ins * 1024, krs, off);
-      lds_dma16(vl + ins * 1024, vrs, off);
-    }
-  };
-  // Block-table entries of the step at key tb (scalar loads, or per-lane
-  // vector loads for kKeyBlocks, fetched a step ahead: the loop's wait before
-  // the barrier covers them). With CLAMPED a key outside [key_begin, key_end)
-  // takes the entry of the nearest such key, so that only blocks the request
-  // owns are read; its keys are masked (and their V rows zeroed).
   auto entry_of = [&](int tb) {
     Entries en;
 #pragma unroll
@@ -245,22 +214,52 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     }
     return en;
   };
-
-  auto consume = [&](int tb, const char* kt, char* vt) {
-    if (tb + kKeys > key_end || (CLAMPED && tb < key_begin)) {
-      // Keys past the tile's last row (and, with short blocks, keys before the
-      // window's first, read from the nearest owned block) hold arbitrary pool
-      // data: zero their V rows so that a zero probability cannot meet a
-      // non-finite value. Whole-block keys before the window are stored tokens.
-      for (int p = tid; p < kKeys * S::CPR; p += kPrefillWaves * 64) {
-        const int key = tb + p / S::CPR;
-        if (key >= key_end || (CLAMPED && key < key_begin))
-          *reinterpret_cast<uint4*>(vt + p * 16) = make_uint4(0, 0, 0, 0);
-      }
-      __syncthreads();
+  // Byte offsets of this wave's direct loads for the step at tb, the same for
+  // its K and its V tile. Steps are kKeys-aligned. Piece p = 64 ins + lane of
+  // load instruction ins (wave ins % waves): token p / CPR, stored chunk
+  // p % CPR holding the token's chunk (p % CPR) ^ swz(token, D / 8). A token
+  // outside [key_begin, key_end) reads the row of the nearest token inside:
+  // every row read is a stored token, so the masked keys' V rows are finite
+  // and their zero probabilities contribute exactly zero (no zeroing pass).
+  // The clamped token stays in the block of the entry used for it: blocks of
+  // kKeys or more hold the whole step, shorter blocks whole load instructions
+  // or (kKeyBlocks) the lane's own token, and clamping is monotone.
+  struct Offsets {
+    uint32_t v[LPW];
+  };
+  auto offsets_of = [&](int tb, const Entries& en) {
+    Offsets of{};
+#pragma unroll
+    for (int k = 0; k < LPW; ++k) {
+      const int ins = wave + k * kPrefillWaves;
+      if (S::NI % kPrefillWaves != 0 && ins >= S::NI) break;  // wave-uniform
+      const int p = ins * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
+      const int key = min(max(tb + tt, key_begin), key_end - 1);
+      const uint32_t slot = (uint32_t)((en.e[MODE == kStepBlocks ? 0 : k] << shift) | (key & bmask));
+      of.v[k] = slot * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4);
     }
-    // S^T = K.Q^T: lane (q, c16) gets qrow c16 (+16 nt), keys tb + 16h + 4q + r.
-    f32x4_t sc[kKG][kNT];
+    return of;
+  };
+  auto issue = [&](const Offsets& of, __amdgpu_buffer_rsrc_t rs, char* tile) {
+    // Per-lane entries are vector loads of the previous step, already complete
+    // (the loop waits for every load before its closing barrier); say so to
+    // the compiler.
+    if constexpr (MODE == kKeyBlocks) wait_vmem_visible();
+    const uint32_t base = lds_addr(tile);
+#pragma unroll
+    for (int k = 0; k < LPW; ++k) {
+      const int ins = wave + k * kPrefillWaves;
+      if (S::NI % kPrefillWaves != 0 && ins >= S::NI) break;  // wave-uniform
+      lds_dma16(base + ins * 1024, rs, of.v[k]);
+    }
+  };
+
+  // Scores of the current step and probabilities of the previous one.
+  f32x4_t sc[kKG][kNT];
+  bf16x8_t pa[kKH][kNT];
+
+  // S^T = K.Q^T into sc: lane (q, c16) gets qrow c16 (+16 nt), keys tb + 16h + 4q + r.
+  auto scores = [&](const char* kt) {
 #pragma unroll
     for (int h = 0; h < kKG; ++h) {
       const int tt = 16 * h + c16;
@@ -275,29 +274,48 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
         for (int c = 0; c < S::NC; ++c) sc[h][nt] = mfma32(kr[c], qb[nt][c], sc[h][nt]);
       }
     }
+  };
 
-    // V operand c of P . V for the 32-key half hh: keys 32hh + 4q + (c16 >> 2)
-    // and 32hh + 16 + 4q + (c16 >> 2), dims 16c + 4 (c16 & 3), read transposed.
-    auto read_v = [&](int hh, int c) {
-      const int lc = 2 * c + ((c16 & 3) >> 1);
-      const int t0 = 32 * hh + 4 * q + (c16 >> 2), t1 = t0 + 16;
-      const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3));
-      const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3));
-      return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-    };
-    bf16x8_t vb[kEarlyV ? S::NO : 1];
-    if constexpr (kEarlyV) {
+  // V operand c of P . V for the 32-key half hh of the V tile vt: keys
+  // 32hh + 4q + (c16 >> 2) and 32hh + 16 + 4q + (c16 >> 2), dims
+  // 16c + 4 (c16 & 3), read transposed.
+  auto read_v = [&](const char* vt, int hh, int c) {
+    const int lc = 2 * c + ((c16 & 3) >> 1);
+    const int t0 = 32 * hh + 4 * q + (c16 >> 2), t1 = t0 + 16;
+    const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3));
+    const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz(t1, D / 8)) << 4) + ((c16 & 1) << 3));
+    return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // O[qrow][dim] += P . V with pa and the V tile vt, and the row sums. The
+  // first half's operands come from vfirst when the caller read them earlier.
+  auto accumulate = [&](const char* vt, const bf16x8_t* vfirst) {
 #pragma unroll
-      for (int c = 0; c < S::NO; ++c) vb[c] = read_v(0, c);
+    for (int c = 0; c < S::NO; ++c) {
+#pragma unroll
+      for (int hh = 0; hh < kKH; ++hh) {
+        const bf16x8_t v = (hh == 0 && vfirst) ? vfirst[c] : read_v(vt, hh, c);
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[hh][nt], v, o[nt][c]);
+      }
     }
+    if constexpr (kMfmaSum) {
+      const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
+                             (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
+#pragma unroll
+      for (int hh = 0; hh < kKH; ++hh)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) l_run[nt] = mfma32(pa[hh][nt], ones, l_run[nt]);
+    }
+  };
 
-    // A step whose keys every valid query row of this wave sees (below the
-    // causal diagonal, inside the window) needs no per-element mask. Without
-    // softcap the scale folds into the exponent: masked scores become -inf in
-    // place (the same registers on both paths), the row maximum is taken on raw
-    // scores (scale > 0), and p = exp2(fma(s, scale, -max)).
+  // Online softmax of the step at tb: mask sc, form pa, re-base o and l_run.
+  // A step whose keys every valid query row of this wave sees (below the
+  // causal diagonal, inside the window) needs no per-element mask. Without
+  // softcap the scale folds into the exponent: masked scores become -inf in
+  // place (the same registers on both paths), the row maximum is taken on raw
+  // scores (scale > 0), and p = exp2(fma(s, scale, -max)).
+  auto softmax = [&](int tb) {
     const bool full = !SOFTCAP && tb + kKeys - 1 <= wave_pos_min && tb >= wave_left_max;
-    bf16x8_t pa[kKH][kNT];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
       float mx = -INFINITY;
@@ -369,56 +387,99 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
       }
       if constexpr (!kMfmaSum) l_run[nt][0] += lsum;
     }
-
-    // O[qrow][dim] += P . V, and the row sums.
-#pragma unroll
-    for (int c = 0; c < S::NO; ++c) {
-#pragma unroll
-      for (int hh = 0; hh < kKH; ++hh) {
-        const bf16x8_t v = (kEarlyV && hh == 0) ? vb[kEarlyV ? c : 0] : read_v(hh, c);
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[hh][nt], v, o[nt][c]);
-      }
-    }
-    if constexpr (kMfmaSum) {
-      const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
-                             (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
-#pragma unroll
-      for (int hh = 0; hh < kKH; ++hh)
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) l_run[nt] = mfma32(pa[hh][nt], ones, l_run[nt]);
-    }
   };
 
-  // Two-stage pipeline over the workgroup, one barrier per step: before it
-  // each wave waits for its own loads of the current stage; after it every
-  // wave's loads of the stage have landed and every wave has finished the
-  // previous step, whose buffer is refilled with the next step. (Unrolling the
-  // loop over the two stages, so that each stage's LDS addresses become
-  // immediate offsets, saved address arithmetic but made the register
-  // allocator copy the accumulators on the lazy re-base branch's common edge:
-  // 183.3 against 182.5 us on C4.)
-  static_assert(kStages == 2, "the step loop alternates two stages");
-  Entries e_next{};
-  issue(kb0, entry_of(kb0), kv[0][0], kv[0][1]);
-  if (1 < nsteps) e_next = entry_of(kb0 + kKeys);
-  for (int step = 0; step < nsteps; ++step) {
+  static_assert(kStages == 2, "K and V alternate between two stages");
+  if constexpr (!kPingPong) {
+    // One barrier per step: before it each wave waits for its own loads of
+    // the current stage; after it every wave's loads of the stage have landed
+    // and every wave has finished the previous step, whose stage is refilled
+    // with the next step. The first half's V operands are read before the
+    // softmax, their LDS latency behind its arithmetic. (Unrolling the loop
+    // over the two stages, so that each stage's LDS addresses become
+    // immediate offsets, saved address arithmetic but made the register
+    // allocator copy the accumulators on the lazy re-base branch's common
+    // edge: 183.3 against 182.5 us on C4.)
+    Entries e_next{};
+    {
+      const Offsets first = offsets_of(kb0, entry_of(kb0));
+      issue(first, krs, kv[0][0]);
+      issue(first, vrs, kv[0][1]);
+    }
+    if (1 < nsteps) e_next = entry_of(kb0 + kKeys);
+    for (int step = 0; step < nsteps; ++step) {
+      const int tb = kb0 + step * kKeys;
+      wait_vmem<0>();
+      __syncthreads();
+      // Every load of this wave has landed; tell the compiler. Its wait-count
+      // model does not see the asm direct loads or waits, so it still counts
+      // the query loads before the loop (and, with per-lane entries, the entry
+      // loads) as outstanding, and would put an s_waitcnt vmcnt(0) before
+      // their first use in the step: after this step's direct loads, which it
+      // would then wait for (C4: 185.2 -> 183.9 us).
+      wait_vmem_visible();
+      if (step + 1 < nsteps) {
+        const int next = (step + 1) & 1;
+        const Offsets of = offsets_of(tb + kKeys, e_next);
+        issue(of, krs, kv[next][0]);
+        issue(of, vrs, kv[next][1]);
+        if (step + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
+      }
+      const int cur = step & 1;
+      scores(kv[cur][0]);
+      bf16x8_t vfirst[S::NO];
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) vfirst[c] = read_v(kv[cur][1], 0, c);
+      softmax(tb);
+      accumulate(kv[cur][1], vfirst);
+    }
+  } else {
+    // Two groups of waves, one wave of each on every SIMD (waves w and w + 4
+    // share a SIMD), take turns between the matrix cores and the vector ALU.
+    // A wave's work per step is an MFMA phase M(i) (scores of step i, then
+    // P.V of step i - 1) and a VALU phase S(i) (the softmax of step i), run as
+    // M(0) S(0) M(1) S(1) ... M(n) with a barrier after each phase. The
+    // second group passes one barrier before its first phase and the first
+    // group one after its last, so the second runs every phase one barrier
+    // interval later: between two barriers one wave of each SIMD is in an
+    // MFMA phase while the other is in a softmax phase.
+    //
+    // LDS: a wave's iteration i reads K(i) (stage i % 2) and V(i - 1) (stage
+    // (i - 1) % 2). At its start each wave issues its share of the direct
+    // loads of K(i + 1) and V(i), into the stages that both groups last read
+    // in iteration i - 1, and waits for them before the barrier that ends
+    // interval 2i + 1 (the first group's second barrier of the iteration, the
+    // second group's first), after which the first group reads them.
+    const bool lead = wave < kPrefillWaves / 2;
+    Entries e_next = entry_of(kb0);
+    Offsets off_v = offsets_of(kb0, e_next);  // offsets of the step whose V is issued next
+    issue(off_v, krs, kv[0][0]);
+    if (1 < nsteps) e_next = entry_of(kb0 + kKeys);
     wait_vmem<0>();
     __syncthreads();
-    // Every load of this wave has landed; tell the compiler. Its wait-count
-    // model does not see the asm direct loads or waits, so it still counts the
-    // query loads before the loop (and, with per-lane entries, the entry loads)
-    // as outstanding, and would put an s_waitcnt vmcnt(0) before their first
-    // use in the step: after this step's direct loads, which it would then
-    // wait for (C4: 185.2 -> 183.9 us).
-    wait_vmem_visible();
-    if (step + 1 < nsteps) {
-      const int next = (step + 1) & 1;
-      issue(kb0 + (step + 1) * kKeys, e_next, kv[next][0], kv[next][1]);
-      if (step + 2 < nsteps) e_next = entry_of(kb0 + (step + 2) * kKeys);
+    wait_vmem_visible();  // as in the other loop: the query (and entry) loads have landed
+    if (!lead) __syncthreads();
+    for (int i = 0; i <= nsteps; ++i) {
+      const int tb = kb0 + i * kKeys;
+      if (i + 1 < nsteps) {
+        const Offsets off_k = offsets_of(tb + kKeys, e_next);
+        issue(off_k, krs, kv[(i + 1) & 1][0]);
+        issue(off_v, vrs, kv[i & 1][1]);
+        off_v = off_k;
+        if (i + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
+      } else if (i + 1 == nsteps) {
+        issue(off_v, vrs, kv[i & 1][1]);
+      }
+      if (i < nsteps) scores(kv[i & 1][0]);
+      if (i > 0) accumulate(kv[(i - 1) & 1][1], nullptr);
+      if (!lead) wait_vmem<0>();
+      __syncthreads();
+      if (i < nsteps) softmax(tb);
+      if (lead) wait_vmem<0>();
+      __syncthreads();
+      wait_vmem_visible();
     }
-    const int cur = step & 1;
-    consume(kb0 + step * kKeys, kv[cur][0], kv[cur][1]);
+    if (lead) __syncthreads();
   }
 
   // Normalise and store: o row 4q + r of tile nt, its sum in l_run[nt][r]
