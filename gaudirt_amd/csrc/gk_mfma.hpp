@@ -10,6 +10,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -20,7 +21,6 @@ __device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret
 
 // 16 bytes of a K/V row that is read once: a non-temporal load.
 __device__ __forceinline__ uint4 load16_once(const uint16_t* p) {
-  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
@@ -67,6 +67,30 @@ __device__ __forceinline__ float max2(float a, float b) {
   float r;
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
+}
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// Maximum of N >= 2 values as a tree of bare max3 (depth log3 N): a chain
+// would be N / 2 dependent instructions, and fmaxf would quiet every input
+// first.
+template <int N>
+__device__ __forceinline__ float tree_max(const float (&v)[N]) {
+  static_assert(N >= 2, "at least two values");
+  if constexpr (N == 2) {
+    return max2(v[0], v[1]);
+  } else {
+    constexpr int M = (N + 2) / 3;
+    float w[M];
+#pragma unroll
+    for (int i = 0; i < N / 3; ++i) w[i] = max3(v[3 * i], v[3 * i + 1], v[3 * i + 2]);
+    if constexpr (N % 3 == 1) w[M - 1] = v[N - 1];
+    if constexpr (N % 3 == 2) w[M - 1] = max2(v[N - 2], v[N - 1]);
+    if constexpr (M == 1) return w[0];
+    else return tree_max<M>(w);
+  }
 }
 __device__ __forceinline__ float col4_max(float x) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

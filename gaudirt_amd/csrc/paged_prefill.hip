@@ -316,62 +316,77 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // scores (scale > 0), and p = exp2(fma(s, scale, -max)).
   auto softmax = [&](int tb) {
     const bool full = !SOFTCAP && tb + kKeys - 1 <= wave_pos_min && tb >= wave_left_max;
+    // Mask, and each tile's row maximum over this lane's 4 kKG scores.
+    float mx[kNT];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
-      float mx = -INFINITY;
       if constexpr (SOFTCAP) {
 #pragma unroll
         for (int h = 0; h < kKG; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int key = tb + 16 * h + 4 * q + r;
-            float s = a.softcap_log2 * soft_tanh(sc[h][nt][r] * a.score_scale);
-            s = (key <= qpos[nt] && key >= qleft[nt]) ? s : -INFINITY;
-            sc[h][nt][r] = s;
-            mx = fmaxf(mx, s);
+            const float sv = a.softcap_log2 * soft_tanh(sc[h][nt][r] * a.score_scale);
+            sc[h][nt][r] = (key <= qpos[nt] && key >= qleft[nt]) ? sv : -INFINITY;
           }
-      } else {
-        if (!full) {
-#pragma unroll
-          for (int h = 0; h < kKG; ++h)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int key = tb + 16 * h + 4 * q + r;
-              sc[h][nt][r] = (key <= qpos[nt] && key >= qleft[nt]) ? sc[h][nt][r] : -INFINITY;
-            }
-        }
+      } else if (!full) {
 #pragma unroll
         for (int h = 0; h < kKG; ++h)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[h][nt][r]);
-        mx *= a.score_scale;
+          for (int r = 0; r < 4; ++r) {
+            const int key = tb + 16 * h + 4 * q + r;
+            sc[h][nt][r] = (key <= qpos[nt] && key >= qleft[nt]) ? sc[h][nt][r] : -INFINITY;
+          }
       }
-      // The probabilities are formed right away against the running maximum;
-      // the step's maximum is reduced across lanes alongside them and only
-      // decides afterwards whether the (rare) re-base is due, which then
-      // recomputes them against the new maximum. Same values as re-basing
-      // first; the exponentials no longer wait for the cross-lane reduction.
-      auto probabilities = [&](float base) {
-        float ps[4 * kKG];
+      float t[4 * kKG];
 #pragma unroll
-        for (int i = 0; i < 4 * kKG; ++i) {
-          if constexpr (SOFTCAP) ps[i] = fast_exp2(sc[i >> 2][nt][i & 3] - base);
-          else ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
+      for (int i = 0; i < 4 * kKG; ++i) t[i] = sc[i >> 2][nt][i & 3];
+      const float m = tree_max(t);
+      mx[nt] = SOFTCAP ? m : m * a.score_scale;
+    }
+    // The probabilities of both tiles are formed right away against the
+    // running maxima, before the cross-lane reduction of the steps' maxima,
+    // which only decides afterwards whether a (rare) re-base is due; that
+    // recomputes them against the new maximum. Same values as re-basing
+    // first. In the ping-pong loop empty asm uses keep them above the re-base
+    // branches, which the compiler would otherwise sink them into, behind the
+    // reduction (C4 shapes at head_dim 64: 107.2 -> 105.4 us); at head_dim 128
+    // that order measured 0.8% slower.
+    auto probabilities = [&](int nt, float base) {
+      float ps[4 * kKG];
+#pragma unroll
+      for (int i = 0; i < 4 * kKG; ++i) {
+        if constexpr (SOFTCAP) ps[i] = fast_exp2(sc[i >> 2][nt][i & 3] - base);
+        else ps[i] = fast_exp2(__builtin_fmaf(sc[i >> 2][nt][i & 3], a.score_scale, -base));
+      }
+#pragma unroll
+      for (int i = 0; i < 4 * kKG; ++i) pa[i >> 3][nt][i & 7] = (__bf16)ps[i];
+      if constexpr (!kMfmaSum) {
+        float l = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4 * kKG; ++i) l += ps[i];
+        return l;
+      }
+      return 0.f;
+    };
+    float lsum[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      lsum[nt] = probabilities(nt, m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
+      if constexpr (kPingPong) {
+#pragma unroll
+        for (int hh = 0; hh < kKH; ++hh) {
+          const auto w = __builtin_bit_cast(u32x4_t, pa[hh][nt]);
+          asm volatile("" ::"v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]));
         }
+      }
+    }
 #pragma unroll
-        for (int i = 0; i < 4 * kKG; ++i) pa[i >> 3][nt][i & 7] = (__bf16)ps[i];
-        if constexpr (!kMfmaSum) {
-          float l = 0.f;
+    for (int nt = 0; nt < kNT; ++nt) mx[nt] = col4_max(mx[nt]);
 #pragma unroll
-          for (int i = 0; i < 4 * kKG; ++i) l += ps[i];
-          return l;
-        }
-        return 0.f;
-      };
-      float lsum = probabilities(m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
-      mx = col4_max(mx);
-      if (__builtin_amdgcn_ballot_w64(mx > m_run[nt] + kLazyRescale)) {
-        const float m_new = fmaxf(m_run[nt], mx);
+    for (int nt = 0; nt < kNT; ++nt) {
+      if (__builtin_amdgcn_ballot_w64(mx[nt] > m_run[nt] + kLazyRescale)) {
+        const float m_new = fmaxf(m_run[nt], mx[nt]);
         const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
         m_run[nt] = m_new;
         if constexpr (!kMfmaSum) l_run[nt][0] *= alpha;
@@ -383,9 +398,9 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
           for (int c = 0; c < S::NO; ++c) o[nt][c][r] *= f;
           if constexpr (kMfmaSum) l_run[nt][r] *= f;
         }
-        lsum = probabilities(m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
+        lsum[nt] = probabilities(nt, m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
       }
-      if constexpr (!kMfmaSum) l_run[nt][0] += lsum;
+      if constexpr (!kMfmaSum) l_run[nt][0] += lsum[nt];
     }
   };
 
