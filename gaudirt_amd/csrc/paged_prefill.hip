@@ -111,7 +111,13 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // kStages K/V stages. The direct loads are asm statements the compiler does
   // not track, so one array serves every stage; reads are ordered by the
   // explicit vmcnt wait and the barrier of each step.
-  __shared__ __attribute__((aligned(16))) char kv[kStages][2][S::TILE];
+  // The same LDS holds, after the step loop, each wave's output rows in bf16
+  // (rows padded by 16 bytes so that the four q-groups' rows of a write fall
+  // on different banks), read back as 16-byte pieces for the global stores.
+  constexpr int kOutRowBytes = 2 * D + 16;
+  constexpr int kKvBytes = kStages * 2 * S::TILE, kOutBytes = kPrefillWaves * kQrowsPerWave * kOutRowBytes;
+  __shared__ __attribute__((aligned(16))) char lds[kKvBytes > kOutBytes ? kKvBytes : kOutBytes];
+  auto kv = reinterpret_cast<char(*)[2][S::TILE]>(lds);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS bases of the direct loads)
@@ -348,10 +354,11 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     // running maxima, before the cross-lane reduction of the steps' maxima,
     // which only decides afterwards whether a (rare) re-base is due; that
     // recomputes them against the new maximum. Same values as re-basing
-    // first. In the ping-pong loop empty asm uses keep them above the re-base
-    // branches, which the compiler would otherwise sink them into, behind the
-    // reduction (C4 shapes at head_dim 64: 107.2 -> 105.4 us); at head_dim 128
-    // that order measured 0.8% slower.
+    // first. Empty asm uses keep them above the re-base branch, which the
+    // compiler would otherwise sink them into, behind the reduction (C4 shapes
+    // at head_dim 64: 107.2 -> 105.4 us). One branch serves both tiles, so the
+    // common path of a step is one basic block (head_dim 128: 156.3 ->
+    // 154.9 us against a branch per tile).
     auto probabilities = [&](int nt, float base) {
       float ps[4 * kKG];
 #pragma unroll
@@ -373,19 +380,21 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
       lsum[nt] = probabilities(nt, m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
-      if constexpr (kPingPong) {
 #pragma unroll
-        for (int hh = 0; hh < kKH; ++hh) {
-          const auto w = __builtin_bit_cast(u32x4_t, pa[hh][nt]);
-          asm volatile("" ::"v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]));
-        }
+      for (int hh = 0; hh < kKH; ++hh) {
+        const auto w = __builtin_bit_cast(u32x4_t, pa[hh][nt]);
+        asm volatile("" ::"v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]));
       }
     }
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) mx[nt] = col4_max(mx[nt]);
+    bool any = false;
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-      if (__builtin_amdgcn_ballot_w64(mx[nt] > m_run[nt] + kLazyRescale)) {
+    for (int nt = 0; nt < kNT; ++nt) any = any || (mx[nt] > m_run[nt] + kLazyRescale);
+    if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        if (!__builtin_amdgcn_ballot_w64(mx[nt] > m_run[nt] + kLazyRescale)) continue;
         const float m_new = fmaxf(m_run[nt], mx[nt]);
         const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
         m_run[nt] = m_new;
@@ -400,8 +409,10 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
         }
         lsum[nt] = probabilities(nt, m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
       }
-      if constexpr (!kMfmaSum) l_run[nt][0] += lsum[nt];
     }
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+      if constexpr (!kMfmaSum) l_run[nt][0] += lsum[nt];
   };
 
   static_assert(kStages == 2, "K and V alternate between two stages");
@@ -497,8 +508,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     if (lead) __syncthreads();
   }
 
-  // Normalise and store: o row 4q + r of tile nt, its sum in l_run[nt][r]
-  // (MFMA sums) or in lane c16 == 4q + r after the cross-row sum (VALU sums).
+  // Normalise into bf16 rows in LDS: o row 4q + r of tile nt, its sum in
+  // l_run[nt][r] (MFMA sums) or in lane c16 == 4q + r after the cross-row sum
+  // (VALU sums). Then each wave stores its own rows as 16-byte pieces: the
+  // wave's LDS operations complete in order, so it reads back what it wrote.
+  // (Stored straight from the MFMA layout, a lane's values are 2-byte
+  // elements 32 bytes apart: 64 narrow stores per lane.)
+  __syncthreads();  // every wave has finished reading the K/V stages
+  char* rows_lds = lds + wave * kQrowsPerWave * kOutRowBytes;
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
     float l = 0.f;
@@ -507,14 +524,23 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     for (int r = 0; r < 4; ++r) {
       const float lr = kMfmaSum ? l_run[nt][r]
                                 : __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l)));
-      const int qr = wave * kQrowsPerWave + nt * 16 + 4 * q + r;
-      const int row = qr / g, head = qr % g;
-      if (row >= nr) continue;
       const float inv = lr > 0.f ? 1.f / lr : 0.f;
-      uint16_t* dst = a.out + (int64_t)(first_row + row) * a.out_stride + (int64_t)(kvh * g + head) * D + c16;
+      __bf16* dst = reinterpret_cast<__bf16*>(rows_lds + (nt * 16 + 4 * q + r) * kOutRowBytes) + c16;
 #pragma unroll
-      for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(o[nt][c][r] * inv);
+      for (int c = 0; c < S::NO; ++c) dst[16 * c] = (__bf16)(o[nt][c][r] * inv);
     }
+  }
+  constexpr int kPieces = kQrowsPerWave * D / 8;  // 16-byte pieces of the wave's rows
+  static_assert(kPieces % 64 == 0, "whole pieces per lane");
+#pragma unroll
+  for (int i = 0; i < kPieces / 64; ++i) {
+    const int piece = i * 64 + lane, ql = piece / (D / 8), part = piece % (D / 8);
+    const int qr = wave * kQrowsPerWave + ql;
+    const int row = qr / g, head = qr % g;
+    const uint4 v = *reinterpret_cast<const uint4*>(rows_lds + ql * kOutRowBytes + part * 16);
+    if (row < nr)
+      *reinterpret_cast<uint4*>(a.out + (int64_t)(first_row + row) * a.out_stride + (int64_t)(kvh * g + head) * D +
+                                part * 8) = v;
   }
 }
 
@@ -555,9 +581,10 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
       !p->seq_prefix || !p->out)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: null pointer");
   const auto misaligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) != 0; };
-  if (misaligned(p->query) || misaligned(p->pool) || (p->q_row_stride & 7) ||
-      p->q_row_stride < (int64_t)p->q_heads * p->head_dim || p->out_row_stride < (int64_t)p->q_heads * p->head_dim)
-    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: query/pool must be 16-byte aligned with full rows");
+  if (misaligned(p->query) || misaligned(p->pool) || misaligned(p->out) || (p->q_row_stride & 7) ||
+      (p->out_row_stride & 7) || p->q_row_stride < (int64_t)p->q_heads * p->head_dim ||
+      p->out_row_stride < (int64_t)p->q_heads * p->head_dim)
+    return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: query/pool/out must be 16-byte aligned with full rows");
   PrefillArgs a{};
   a.query = static_cast<const uint16_t*>(p->query);
   a.q_stride = p->q_row_stride;
