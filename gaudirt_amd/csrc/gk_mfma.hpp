@@ -39,20 +39,27 @@ __device__ __forceinline__ int slot_of(const int32_t* s_bt, int b0, int shift, i
 
 // Token swizzle of 16-byte chunks inside an LDS row of a K or V tile: chunk c
 // of token t is stored at c ^ swz(t, CPR) (CPR = 16-byte chunks per row).
-// gfx950's LDS serves 256 bytes per clock (64 banks), so a row of d >= 128
-// bf16 starts every 256 bytes at bank 0 and the swizzle has to spread:
-//  - the 16-key operand reads (16 lanes, 16 consecutive tokens, one logical
-//    chunk each): 16 distinct chunk slots;
+// Bank behaviour measured on gfx950 with SQ_LDS_BANK_CONFLICT, rows of 256
+// bytes (d 128): ds_read_b128 serves 32 lanes at a time over 128 four-byte
+// banks (two tokens per 512-byte bank row), ds_read_b64_tr_b16 32 lanes at a
+// time over 64 banks. The two reads of a tile therefore need:
+//  - the 16-key operand reads (lanes q = 0, 1 of a 32-lane half: 16
+//    consecutive tokens, logical chunks 4c + q): swz(t) >> 1 distinct among
+//    the eight tokens of each parity in an aligned group of 16;
 //  - the transposed 4-token reads of P.V (32 lanes, 8 consecutive tokens, an
-//    aligned pair of chunks each): 8 distinct pair slots.
-// swz = ((t & 7) << 1) | ((t >> 3) & 1) does both. With d = 64 (8 chunks, two
-// rows per 256 bytes) the 3-bit form ((t & 3) << 1) | ((t >> 2) & 1) keeps the
-// chunk inside the row.
+//    aligned pair of chunks each): swz(t) >> 1 distinct over each aligned
+//    group of 8 tokens.
+// swz = (t0 << 1) ^ (t1 << 3) ^ (t2 << 2) ^ (t3 << 1) (bits of t) does both:
+// both reads conflict-free. The previous form ((t & 7) << 1) | (t >> 3) met
+// only the second and spent half the operand reads' LDS cycles in conflicts.
+// With d = 64 (8 chunks, two rows per 256 bytes) the 3-bit form
+// ((t & 3) << 1) | ((t >> 2) & 1) keeps the chunk inside the row.
 // (cpr is a compile-time constant at every call site, written D / 8: passing a
 // static member such as MfmaShape<D>::CPR from a lambda inside a kernel template
 // makes the host pass of hipcc drop the kernel's launch stub.)
 __device__ __forceinline__ int swz(int t, int cpr) {
-  return cpr >= 16 ? (((t & 7) << 1) | ((t >> 3) & 1)) : (((t & 3) << 1) | ((t >> 2) & 1));
+  return cpr >= 16 ? (((t & 1) << 1) ^ ((t & 2) << 2) ^ (t & 4) ^ ((t & 8) >> 2))
+                   : (((t & 3) << 1) | ((t >> 2) & 1));
 }
 
 // Max / sum over the four lanes c, c + 16, c + 32, c + 48 of a column of the
