@@ -52,14 +52,15 @@ __device__ __forceinline__ int slot_of(const int32_t* s_bt, int b0, int shift, i
 // swz = (t0 << 1) ^ (t1 << 3) ^ (t2 << 2) ^ (t3 << 1) (bits of t) does both:
 // both reads conflict-free. The previous form ((t & 7) << 1) | (t >> 3) met
 // only the second and spent half the operand reads' LDS cycles in conflicts.
-// With d = 64 (8 chunks, two rows per 256 bytes) the 3-bit form
-// ((t & 3) << 1) | ((t >> 2) & 1) keeps the chunk inside the row.
+// With d = 64 (8 chunks, 128-byte rows) swz = t & 7 keeps the chunk inside
+// the row and is conflict-free for both reads in the same measurement (the
+// form ((t & 3) << 1) | ((t >> 2) & 1) used before: 2-way on both).
 // (cpr is a compile-time constant at every call site, written D / 8: passing a
 // static member such as MfmaShape<D>::CPR from a lambda inside a kernel template
 // makes the host pass of hipcc drop the kernel's launch stub.)
 __device__ __forceinline__ int swz(int t, int cpr) {
   return cpr >= 16 ? (((t & 1) << 1) ^ ((t & 2) << 2) ^ (t & 4) ^ ((t & 8) >> 2))
-                   : (((t & 3) << 1) | ((t >> 2) & 1));
+                   : (t & 7);
 }
 
 // Max / sum over the four lanes c, c + 16, c + 32, c + 48 of a column of the
