@@ -161,6 +161,29 @@ __device__ __forceinline__ void lds_dma16(uint32_t lds, __amdgpu_buffer_rsrc_t r
       : "memory");
 }
 
+// A raw buffer resource (stride 0, `bytes` records) as four words made
+// wave-uniform with readfirstlane, for lds_dma16_w: where the compiler cannot
+// see that a resource is uniform (e.g. after unrolling a loop whose body takes
+// it from a lambda capture) it keeps __amdgpu_buffer_rsrc_t in VGPRs, which
+// the direct-load asm cannot take.
+__device__ __forceinline__ u32x4_t buffer_words(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u32x4_t w;
+  w[0] = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  w[1] = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32) & 0xffffu);
+  w[2] = __builtin_amdgcn_readfirstlane(bytes);
+  w[3] = (uint32_t)kBufferDword3;
+  return w;
+}
+__device__ __forceinline__ void lds_dma16_w(uint32_t lds, u32x4_t rsrc, uint32_t voffset) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds),
+      "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+
 // The same load for K/V rows that a decode step reads exactly once, with the
 // cache policy GK_KV_LOAD_POLICY: sc1 (device scope: the line is not kept in
 // the CU's vector L1) and nt (non-temporal: streamed through L2 rather than

@@ -28,6 +28,7 @@
 #include "work_order.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace gk {
 namespace {
@@ -196,8 +197,15 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   const uint16_t* kbase = a.pool + (int64_t)kvh * a.slots * D;
   const uint16_t* vbase = kbase + (int64_t)a.kv_heads * a.slots * D;
   const uint32_t region = (uint32_t)(a.slots * D * 2);
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, region, kBufferDword3);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, region, kBufferDword3);
+  // The unrolled d 128 loop passes the resources to the direct-load asm as
+  // words made uniform with readfirstlane (the compiler keeps the opaque
+  // resource in VGPRs there); d 64 keeps the builtin resource (1.8% faster).
+  auto make_rsrc = [&](const uint16_t* base) {
+    if constexpr (D < 128) return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, region, kBufferDword3);
+    else return buffer_words(base, region);
+  };
+  using Rsrc = decltype(make_rsrc(kbase));
+  const Rsrc krs = make_rsrc(kbase), vrs = make_rsrc(vbase);
   const int shift = a.block_shift, bmask = (1 << shift) - 1;
 
   // Block-table entries of the step at key tb (scalar loads, or per-lane
@@ -207,7 +215,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   struct Entries {
     int e[NE];
   };
-  auto entry_of = [&](int tb) {
+  auto entry_of = [&](int tb) __attribute__((always_inline)) {
     Entries en;
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
@@ -233,7 +241,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   struct Offsets {
     uint32_t v[LPW];
   };
-  auto offsets_of = [&](int tb, const Entries& en) {
+  auto offsets_of = [&](int tb, const Entries& en) __attribute__((always_inline)) {
     Offsets of{};
 #pragma unroll
     for (int k = 0; k < LPW; ++k) {
@@ -246,7 +254,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     }
     return of;
   };
-  auto issue = [&](const Offsets& of, __amdgpu_buffer_rsrc_t rs, char* tile) {
+  auto issue = [&](const Offsets& of, Rsrc rs, char* tile) __attribute__((always_inline)) {
     // Per-lane entries are vector loads of the previous step, already complete
     // (the loop waits for every load before its closing barrier); say so to
     // the compiler.
@@ -256,7 +264,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     for (int k = 0; k < LPW; ++k) {
       const int ins = wave + k * kPrefillWaves;
       if (S::NI % kPrefillWaves != 0 && ins >= S::NI) break;  // wave-uniform
-      lds_dma16(base + ins * 1024, rs, of.v[k]);
+      if constexpr (D < 128) lds_dma16(base + ins * 1024, rs, of.v[k]);
+      else lds_dma16_w(base + ins * 1024, rs, of.v[k]);
     }
   };
 
@@ -265,7 +274,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   bf16x8_t pa[kKH][kNT];
 
   // S^T = K.Q^T into sc: lane (q, c16) gets qrow c16 (+16 nt), keys tb + 16h + 4q + r.
-  auto scores = [&](const char* kt) {
+  auto scores = [&](const char* kt) __attribute__((always_inline)) {
 #pragma unroll
     for (int h = 0; h < kKG; ++h) {
       const int tt = 16 * h + c16;
@@ -285,7 +294,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // V operand c of P . V for the 32-key half hh of the V tile vt: keys
   // 32hh + 4q + (c16 >> 2) and 32hh + 16 + 4q + (c16 >> 2), dims
   // 16c + 4 (c16 & 3), read transposed.
-  auto read_v = [&](const char* vt, int hh, int c) {
+  auto read_v = [&](const char* vt, int hh, int c) __attribute__((always_inline)) {
     const int lc = 2 * c + ((c16 & 3) >> 1);
     const int t0 = 32 * hh + 4 * q + (c16 >> 2), t1 = t0 + 16;
     const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz(t0, D / 8)) << 4) + ((c16 & 1) << 3));
@@ -294,7 +303,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   };
   // O[qrow][dim] += P . V with pa and the V tile vt, and the row sums. The
   // first half's operands come from vfirst when the caller read them earlier.
-  auto accumulate = [&](const char* vt, const bf16x8_t* vfirst) {
+  auto accumulate = [&](const char* vt, const bf16x8_t* vfirst) __attribute__((always_inline)) {
 #pragma unroll
     for (int c = 0; c < S::NO; ++c) {
 #pragma unroll
@@ -320,7 +329,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // softcap the scale folds into the exponent: masked scores become -inf in
   // place (the same registers on both paths), the row maximum is taken on raw
   // scores (scale > 0), and p = exp2(fma(s, scale, -max)).
-  auto softmax = [&](int tb) {
+  auto softmax = [&](int tb) __attribute__((always_inline)) {
     const bool full = !SOFTCAP && tb + kKeys - 1 <= wave_pos_min && tb >= wave_left_max;
     // Mask, and each tile's row maximum over this lane's 4 kKG scores.
     float mx[kNT];
@@ -359,7 +368,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     // at head_dim 64: 107.2 -> 105.4 us). One branch serves both tiles, so the
     // common path of a step is one basic block (head_dim 128: 156.3 ->
     // 154.9 us against a branch per tile).
-    auto probabilities = [&](int nt, float base) {
+    auto probabilities = [&](int nt, float base) __attribute__((always_inline)) {
       float ps[4 * kKG];
 #pragma unroll
       for (int i = 0; i < 4 * kKG; ++i) {
@@ -421,11 +430,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     // the current stage; after it every wave's loads of the stage have landed
     // and every wave has finished the previous step, whose stage is refilled
     // with the next step. The first half's V operands are read before the
-    // softmax, their LDS latency behind its arithmetic. (Unrolling the loop
-    // over the two stages, so that each stage's LDS addresses become
-    // immediate offsets, saved address arithmetic but made the register
-    // allocator copy the accumulators on the lazy re-base branch's common
-    // edge: 183.3 against 182.5 us on C4.)
+    // softmax, their LDS latency behind its arithmetic.
     Entries e_next{};
     {
       const Offsets first = offsets_of(kb0, entry_of(kb0));
@@ -433,7 +438,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
       issue(first, vrs, kv[0][1]);
     }
     if (1 < nsteps) e_next = entry_of(kb0 + kKeys);
-    for (int step = 0; step < nsteps; ++step) {
+    // The loop is unrolled over the two stages, so that every LDS address of a
+    // step is a per-lane offset plus an immediate (stage, 16-key group, half):
+    // ~44 fewer VALU instructions per wave and step (C4: 148.6 -> 138.0 us).
+    // The lambdas are forced inline (with three call sites the compiler made
+    // the softmax a real call with a stack frame) and the buffer resources go
+    // to the direct-load asm as scalar words (make_rsrc).
+    auto body = [&](int step, auto stage) __attribute__((always_inline)) {
+      constexpr int cur = decltype(stage)::value, next = cur ^ 1;
       const int tb = kb0 + step * kKeys;
       wait_vmem<0>();
       __syncthreads();
@@ -445,20 +457,24 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
       // would then wait for (C4: 185.2 -> 183.9 us).
       wait_vmem_visible();
       if (step + 1 < nsteps) {
-        const int next = (step + 1) & 1;
         const Offsets of = offsets_of(tb + kKeys, e_next);
         issue(of, krs, kv[next][0]);
         issue(of, vrs, kv[next][1]);
         if (step + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
       }
-      const int cur = step & 1;
       scores(kv[cur][0]);
       bf16x8_t vfirst[S::NO];
 #pragma unroll
       for (int c = 0; c < S::NO; ++c) vfirst[c] = read_v(kv[cur][1], 0, c);
       softmax(tb);
       accumulate(kv[cur][1], vfirst);
+    };
+    int step = 0;
+    for (; step + 1 < nsteps; step += 2) {
+      body(step, std::integral_constant<int, 0>{});
+      body(step + 1, std::integral_constant<int, 1>{});
     }
+    if (step < nsteps) body(step, std::integral_constant<int, 0>{});
   } else {
     // Two groups of waves, one wave of each on every SIMD (waves w and w + 4
     // share a SIMD), take turns between the matrix cores and the vector ALU.
