@@ -89,6 +89,24 @@ def test_struct_size_guard_rejects_mismatched_callers(lib):
     assert "struct_size" in lib.gk_last_error().decode()
 
 
+def test_prefill_alignment_validation(lib):
+    # query, pool and out must be 16-byte aligned with row strides in whole
+    # 16-byte pieces (the kernel writes its output rows as 16-byte stores);
+    # checked on the host before anything is launched.
+    q = capi.PrefillParams()
+    q.q_heads, q.kv_heads, q.head_dim, q.block_size, q.slots, q.scale = 8, 2, 128, 128, 8192, 0.1
+    q.seqs, q.max_rows, q.bt_stride = 1, 4, 8
+    for name in ("query", "pool", "block_tables", "seq_request", "seq_first_row", "seq_rows", "seq_prefix", "out"):
+        setattr(q, name, 256)
+    q.q_row_stride = q.out_row_stride = 8 * 128
+    for field, value in (("out", 258), ("out_row_stride", 8 * 128 + 4), ("query", 264), ("q_row_stride", 8 * 128 + 2)):
+        saved = getattr(q, field)
+        setattr(q, field, value)
+        assert lib.gk_paged_prefill(ctypes.byref(q), None) == capi.GK_ERR_INVALID_ARGUMENT, field
+        assert "16-byte aligned" in lib.gk_last_error().decode(), field
+        setattr(q, field, saved)
+
+
 def test_metadata_and_allocator_validation(lib):
     p = capi.MetadataParams()
     p.struct_size = 16
