@@ -8,32 +8,35 @@
 // tests/fixed_kv_descriptor_device_test.cpp:146-197).
 #include "gk_common.hpp"
 
+#include <algorithm>
+
 namespace gk {
 namespace {
 
-// One thread per 16-byte piece: index = ((row * 2 + kind) * kv_heads + head) * chunks + chunk.
+// One thread per 16-byte piece of a row: workgroup (x, y) takes pieces
+// 256 x .. 256 x + 255 of rows y, y + gridDim.y, ...; piece p of a row is
+// chunk p % chunks of head (p / chunks) % kv_heads of K (p / chunks <
+// kv_heads) or V. The row's slot is a scalar load issued with the piece's
+// load: one memory round trip before the store, no 64-bit index division.
 __global__ __launch_bounds__(256) void kv_store_kernel(const uint16_t* __restrict__ key,
                                                        const uint16_t* __restrict__ value,
                                                        int64_t key_stride, int64_t value_stride,
                                                        const int32_t* __restrict__ slot_mapping,
                                                        int32_t rows, uint16_t* __restrict__ pool,
-                                                       int64_t slots, int32_t kv_heads, int32_t head_dim) {
-  const int32_t chunks = head_dim >> 3;
-  const int64_t total = (int64_t)rows * 2 * kv_heads * chunks;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int32_t chunk = (int32_t)(i % chunks);
-    int64_t rest = i / chunks;
-    const int32_t head = (int32_t)(rest % kv_heads);
-    rest /= kv_heads;
-    const int32_t kind = (int32_t)(rest & 1);
-    const int32_t row = (int32_t)(rest >> 1);
+                                                       int64_t slots, int32_t kv_heads, int32_t chunk_shift) {
+  const int32_t p = (int32_t)blockIdx.x * 256 + (int32_t)threadIdx.x;
+  if (p >= (2 * kv_heads) << chunk_shift) return;
+  const int32_t chunk = p & ((1 << chunk_shift) - 1), kh = p >> chunk_shift;
+  const int32_t kind = kh >= kv_heads ? 1 : 0, head = kh - kind * kv_heads;
+  const int32_t head_dim = 8 << chunk_shift;
+  for (int32_t row = (int32_t)blockIdx.y; row < rows; row += (int32_t)gridDim.y) {
     const int32_t slot = slot_mapping[row];
-    if (slot < 0 || slot >= slots) continue;  // negative: no store; past the pool: never written
     const uint16_t* src = (kind ? value + row * value_stride : key + row * key_stride) +
                           (int64_t)head * head_dim + chunk * 8;
+    const uint4 v = *reinterpret_cast<const uint4*>(src);
+    if (slot < 0 || slot >= slots) continue;  // negative: no store; past the pool: never written
     uint16_t* dst = pool + (((int64_t)kind * kv_heads + head) * slots + slot) * head_dim + chunk * 8;
-    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+    *reinterpret_cast<uint4*>(dst) = v;
   }
 }
 
@@ -79,12 +82,12 @@ int launch_kv_store(const void* key, const void* value, int64_t key_stride, int6
   if (!aligned16(key) || !aligned16(value) || !aligned16(pool) || (key_stride & 7) || (value_stride & 7) ||
       key_stride < (int64_t)kv_heads * head_dim || value_stride < (int64_t)kv_heads * head_dim)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_kv_store: K/V rows must be 16-byte aligned and hold kv_heads * head_dim");
-  const int64_t total = (int64_t)rows * 2 * kv_heads * (head_dim / 8);
-  const int64_t blocks = (total + 255) / 256;
-  const int grid = (int)(blocks < 65536 ? blocks : 65536);
+  if (kv_heads > (1 << 20)) return fail(GK_ERR_INVALID_ARGUMENT, "gk_kv_store: invalid geometry");
+  const int chunk_shift = head_dim == 64 ? 3 : head_dim == 128 ? 4 : 5;
+  const dim3 grid((unsigned)(((2 * kv_heads << chunk_shift) + 255) / 256), (unsigned)std::min(rows, 65535));
   kv_store_kernel<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(key), static_cast<const uint16_t*>(value),
                                             key_stride, value_stride, slot_mapping, rows,
-                                            static_cast<uint16_t*>(pool), slots, kv_heads, head_dim);
+                                            static_cast<uint16_t*>(pool), slots, kv_heads, chunk_shift);
   return hip_status(hipGetLastError(), "gk_kv_store launch");
 }
 
