@@ -27,7 +27,9 @@ def check_against_oracle(case, actual_bits, threads=16):
     assert np.isfinite(orc.bf16_to_f32(actual_bits)).all()
     for name, ref in (("direct_bf16_pv", direct), ("tiled_bf16_pv", tiled)):
         max_abs, mean_abs = orc.check_tolerance(actual_bits, ref, MAX_ABS, MEAN_ABS)
-        print(f"{name}: max_abs={max_abs:.3e} mean_abs={mean_abs:.3e}", flush=True)
+        ulp_only = orc.ulp_allowance_count(actual_bits, ref, MAX_ABS)
+        print(f"{name}: max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} "
+              f"ulp_allowance_only={ulp_only} of {actual_bits.size}", flush=True)
     e64, etiled = orc.isolated_errors(orc.bf16_to_f32(actual_bits), fp64, orc.bf16_to_f32(tiled))
     print(f"isolated_errors: fp64={e64:.3e} tiled={etiled:.3e}", flush=True)
 

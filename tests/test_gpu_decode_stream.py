@@ -38,7 +38,9 @@ def check(case, actual, fp32_softmax=False, rows=None):
         actual, ref = actual[rows], ref[rows]
     assert np.isfinite(orc.bf16_to_f32(actual)).all()
     max_abs, mean_abs = orc.check_tolerance(actual, ref, MAX_ABS, MEAN_ABS)
-    print(f"max_abs={max_abs:.3e} mean_abs={mean_abs:.3e}", flush=True)
+    ulp_only = orc.ulp_allowance_count(actual, ref, MAX_ABS)
+    print(f"max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} ulp_allowance_only={ulp_only} of {actual.size}",
+          flush=True)
     return max_abs, mean_abs
 
 

@@ -38,6 +38,8 @@ def check(case, actual, rows=None, fp32_softmax=False):
     got = actual[sel]
     assert np.isfinite(orc.bf16_to_f32(got)).all()
     max_abs, mean_abs = orc.check_tolerance(got, ref, MAX_ABS, MEAN_ABS)
+    ulp_only = orc.ulp_allowance_count(got, ref, MAX_ABS)
+    print(f"max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} ulp_allowance_only={ulp_only} of {got.size}", flush=True)
     if not fp32_softmax:
         orc.isolated_errors(orc.bf16_to_f32(got), orc.fp64_bf16(p), orc.bf16_to_f32(orc.tiled_bf16_pv(p, 512)))
     return max_abs, mean_abs
