@@ -185,12 +185,18 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   constexpr bool kPingPong = D < 128;
   f32x4_t o[kNT][S::NO];
   float m_run[kNT];
+  // Without softcap the re-base check compares the raw score maximum with
+  // (m_run + kLazyRescale) / scale, kept per tile and updated at each re-base:
+  // the step's maximum is scaled only when a re-base is due.
+  float m_thr[kNT];
+  const float inv_scale = 1.f / a.score_scale;
   f32x4_t l_run[kNT];
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
 #pragma unroll
     for (int c = 0; c < S::NO; ++c) o[nt][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     m_run[nt] = -INFINITY;
+    m_thr[nt] = -INFINITY;
     l_run[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
@@ -356,8 +362,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
       float t[4 * kKG];
 #pragma unroll
       for (int i = 0; i < 4 * kKG; ++i) t[i] = sc[i >> 2][nt][i & 3];
-      const float m = tree_max(t);
-      mx[nt] = SOFTCAP ? m : m * a.score_scale;
+      mx[nt] = tree_max(t);  // log2 units with softcap, raw scores without
     }
     // The probabilities of both tiles are formed right away against the
     // running maxima, before the cross-lane reduction of the steps' maxima,
@@ -399,14 +404,15 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     for (int nt = 0; nt < kNT; ++nt) mx[nt] = col4_max(mx[nt]);
     bool any = false;
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) any = any || (mx[nt] > m_run[nt] + kLazyRescale);
+    for (int nt = 0; nt < kNT; ++nt) any = any || (mx[nt] > (SOFTCAP ? m_run[nt] + kLazyRescale : m_thr[nt]));
     if (__builtin_amdgcn_ballot_w64(any)) {
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt) {
-        if (!__builtin_amdgcn_ballot_w64(mx[nt] > m_run[nt] + kLazyRescale)) continue;
-        const float m_new = fmaxf(m_run[nt], mx[nt]);
+        if (!__builtin_amdgcn_ballot_w64(mx[nt] > (SOFTCAP ? m_run[nt] + kLazyRescale : m_thr[nt]))) continue;
+        const float m_new = fmaxf(m_run[nt], SOFTCAP ? mx[nt] : mx[nt] * a.score_scale);
         const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
         m_run[nt] = m_new;
+        m_thr[nt] = (m_new + kLazyRescale) * inv_scale;
         if constexpr (!kMfmaSum) l_run[nt][0] *= alpha;
         // o rows are qrows 4q + r; qrow h's factor lives in lanes with c16 == h.
 #pragma unroll
