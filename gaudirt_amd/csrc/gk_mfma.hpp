@@ -106,6 +106,21 @@ __device__ __forceinline__ float col4_max(float x) {
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return max2(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
+// col4_max of two values at once (a and b in place). permlane32_swap(a, b)
+// leaves a's lower half next to b's lower half and a's upper half next to
+// b's upper half, so one maximum reduces a over the 32-lane halves in lanes
+// 0-31 and b in lanes 32-63; a 16-lane swap finishes both, and a last 32-lane
+// swap hands every lane both results: 3 permutes and 2 maxima for the 4 and 4
+// of two col4_max calls.
+__device__ __forceinline__ void col4_max2(float& a, float& b) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const float c = max2(__uint_as_float(h[0]), __uint_as_float(h[1]));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+  const float d = max2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto e = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+  a = __uint_as_float(e[0]);
+  b = __uint_as_float(e[1]);
+}
 __device__ __forceinline__ float col4_sum(float x) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = __uint_as_float(a[0]) + __uint_as_float(a[1]);

@@ -190,6 +190,9 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // the step's maximum is scaled only when a re-base is due.
   float m_thr[kNT];
   const float inv_scale = 1.f / a.score_scale;
+  // The base the probabilities are formed against: m_run, or 0 while the row
+  // has no maximum yet (kept with m_run, so a step does not select it).
+  float m_base[kNT];
   f32x4_t l_run[kNT];
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
@@ -197,6 +200,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     for (int c = 0; c < S::NO; ++c) o[nt][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     m_run[nt] = -INFINITY;
     m_thr[nt] = -INFINITY;
+    m_base[nt] = 0.f;
     l_run[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
@@ -393,7 +397,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
     float lsum[kNT];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
-      lsum[nt] = probabilities(nt, m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
+      lsum[nt] = probabilities(nt, m_base[nt]);
 #pragma unroll
       for (int hh = 0; hh < kKH; ++hh) {
         const auto w = __builtin_bit_cast(u32x4_t, pa[hh][nt]);
@@ -401,7 +405,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
       }
     }
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) mx[nt] = col4_max(mx[nt]);
+    for (int nt = 0; nt + 1 < kNT; nt += 2) col4_max2(mx[nt], mx[nt + 1]);
+    if constexpr (kNT % 2) mx[kNT - 1] = col4_max(mx[kNT - 1]);
     bool any = false;
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) any = any || (mx[nt] > (SOFTCAP ? m_run[nt] + kLazyRescale : m_thr[nt]));
@@ -413,6 +418,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
         const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
         m_run[nt] = m_new;
         m_thr[nt] = (m_new + kLazyRescale) * inv_scale;
+        m_base[nt] = m_new == -INFINITY ? 0.f : m_new;
         if constexpr (!kMfmaSum) l_run[nt][0] *= alpha;
         // o rows are qrows 4q + r; qrow h's factor lives in lanes with c16 == h.
 #pragma unroll
@@ -422,7 +428,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
           for (int c = 0; c < S::NO; ++c) o[nt][c][r] *= f;
           if constexpr (kMfmaSum) l_run[nt][r] *= f;
         }
-        lsum[nt] = probabilities(nt, m_run[nt] == -INFINITY ? 0.f : m_run[nt]);
+        lsum[nt] = probabilities(nt, m_base[nt]);
       }
     }
 #pragma unroll
