@@ -253,13 +253,23 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   };
   auto offsets_of = [&](int tb, const Entries& en) __attribute__((always_inline)) {
     Offsets of{};
+    // One block holds the whole step: the clamped key's offset in the step
+    // stays in [0, kKeys) (the first step starts at or below key_begin, the
+    // last holds key_end - 1), so the slot is a scalar base plus that offset.
+    const int lo = key_begin - tb, hi = key_end - 1 - tb;
+    const uint32_t step_slot = ((uint32_t)en.e[0] << shift) + (uint32_t)(tb & bmask);
 #pragma unroll
     for (int k = 0; k < LPW; ++k) {
       const int ins = wave + k * kPrefillWaves;
       if (S::NI % kPrefillWaves != 0 && ins >= S::NI) break;  // wave-uniform
       const int p = ins * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
-      const int key = min(max(tb + tt, key_begin), key_end - 1);
-      const uint32_t slot = (uint32_t)((en.e[MODE == kStepBlocks ? 0 : k] << shift) | (key & bmask));
+      uint32_t slot;
+      if constexpr (MODE == kStepBlocks) {
+        slot = step_slot + (uint32_t)min(max(tt, lo), hi);
+      } else {
+        const int key = min(max(tb + tt, key_begin), key_end - 1);
+        slot = (uint32_t)((en.e[k] << shift) | (key & bmask));
+      }
       of.v[k] = slot * (2 * D) + ((pc ^ swz(tt, D / 8)) << 4);
     }
     return of;
