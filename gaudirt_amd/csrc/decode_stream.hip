@@ -388,6 +388,11 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   bf16x8_t qb[S::NC];
   f32x4_t o[S::NO];
   float m_run = -INFINITY, l_run = 0.f;
+  // Without softcap: (m_run + kDecodeLazyRescale) / scale, the raw-score
+  // threshold of a re-base; and the base of the probabilities (m_run, or 0
+  // before the first maximum). Both change only at a re-base.
+  float m_thr = -INFINITY, m_base = 0.f;
+  const float inv_scale = 1.f / a.score_scale;
 
   // Finished segments are not stored right away. The pipeline's waits count
   // every vector memory operation older than the newest tile (vmcnt), so a
@@ -505,6 +510,8 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       for (int c = 0; c < S::NO; ++c) o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       m_run = -INFINITY;
       l_run = 0.f;
+      m_thr = -INFINITY;
+      m_base = 0.f;
     }
 
     // K tile -> registers as the A operand of S^T: lane (q, c16), group h holds
@@ -525,25 +532,36 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       for (int c = 0; c < S::NC; ++c) sc[h] = mfma32(kr[h][c], qb[c], sc[h]);
     }
 
-    float mx = -INFINITY;
+    // Mask, and the row maximum over this lane's scores. Without softcap the
+    // scores stay raw: a tile whose keys are all visible needs no per-element
+    // mask, the maximum is compared with (m_run + kDecodeLazyRescale) / scale
+    // (kept with m_run), and the scale folds into the exponent below.
+    const bool inside = !SOFTCAP && t.tb >= t.left && t.tb + TS <= t.ctx;  // wave-uniform
+    if (!inside) {
 #pragma unroll
-    for (int h = 0; h < S::TG; ++h)
+      for (int h = 0; h < S::TG; ++h)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s;
-        if constexpr (SOFTCAP) s = a.softcap_log2 * soft_tanh(sc[h][r] * a.score_scale);
-        else s = sc[h][r] * a.score_scale;
-        const int key = t.tb + 16 * h + 4 * q + r;
-        s = (key >= t.left && key < t.ctx) ? s : -INFINITY;
-        sc[h][r] = s;
-        mx = fmaxf(mx, s);
-      }
-    mx = col4_max(mx);
-    if (__builtin_amdgcn_ballot_w64(mx > m_run + kDecodeLazyRescale)) {
-      const float m_new = fmaxf(m_run, mx);
+        for (int r = 0; r < 4; ++r) {
+          float s = sc[h][r];
+          if constexpr (SOFTCAP) s = a.softcap_log2 * soft_tanh(s * a.score_scale);
+          const int key = t.tb + 16 * h + 4 * q + r;
+          sc[h][r] = (key >= t.left && key < t.ctx) ? s : -INFINITY;
+        }
+    }
+    float mx;
+    {
+      float v[4 * S::TG];
+#pragma unroll
+      for (int i = 0; i < 4 * S::TG; ++i) v[i] = sc[i >> 2][i & 3];
+      mx = col4_max(tree_max(v));
+    }
+    if (__builtin_amdgcn_ballot_w64(mx > (SOFTCAP ? m_run + kDecodeLazyRescale : m_thr))) {
+      const float m_new = fmaxf(m_run, SOFTCAP ? mx : mx * a.score_scale);
       const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
       l_run *= alpha;
       m_run = m_new;
+      m_thr = (m_new + kDecodeLazyRescale) * inv_scale;
+      m_base = m_new == -INFINITY ? 0.f : m_new;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float f = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(alpha)));
@@ -551,12 +569,11 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
         for (int c = 0; c < S::NO; ++c) o[c][r] *= f;
       }
     }
-    const float base = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
     for (int h = 0; h < S::TG; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = fast_exp2(sc[h][r] - base);
+        const float p = SOFTCAP ? fast_exp2(sc[h][r] - m_base) : fast_exp2(__builtin_fmaf(sc[h][r], a.score_scale, -m_base));
         sc[h][r] = p;
         l_run += p;
       }
