@@ -10,6 +10,14 @@ Parity status (how each oracle function is pinned; see tests/test_oracle.py):
 
 - ``bf16_from_f32``: torch's CPU ``.to(torch.bfloat16)`` (an independent RNE
   implementation) on random, tie, NaN and overflow inputs.
+Vectors of the reference's own CPU references (tests/golden/reference_vectors.npz,
+written by tests/golden/make_reference_vectors.py from tests/paged_attention_reference.py,
+tests/paged_attention_reference_test.py and tests/fp64_reference.py; checked by
+tests/test_golden.py) pin ``direct_bf16_pv``, ``tiled_bf16_pv``, ``direct_tiled`` and
+``bf16_from_f64`` bit for bit on the reference test's inputs, the C1 case and 2,224
+roundings; on a d 64 chunked-prefill case 15 of 14,336 outputs differ where torch's
+fp32 exp rounds one probability to the neighbouring bf16 value (max abs 9.8e-4).
+
 - ``bf16_from_f64``: the known answer of tests/decoder_cpu_reference_test.py:66-68
   (1 + 2^-8 + 2^-32 -> 1 + 2^-7), exact rational rounding with ``fractions`` on
   random normals, subnormals and ties, the overflow boundary, and rejection of

@@ -169,10 +169,12 @@ def _reference_test_inputs():
 def test_tiled_equals_direct_tiled_on_reference_inputs():
     # tests/paged_attention_reference_test.py:48-50 asserts that the two tiled
     # formulations are bitwise equal. They round differently (probabilities
-    # normalised before vs after the bf16 rounding), and a torch 2.10 CPU
-    # retype of both differs by up to 8 bf16 ulp on near-zero outputs, so the
-    # claim is pinned here as the reference's own tiled gate: per-row relative
-    # L2 within 5e-3 (tests/paged_attention_reference.py:68).
+    # normalised before vs after the bf16 rounding): the reference's own two
+    # functions differ by up to 8 bf16 ulp on these inputs under torch 2.10
+    # (tests/golden/reference_vectors.npz, tests/test_golden.py, where the
+    # oracle matches each of them bit for bit), so the claim is pinned here as
+    # the reference's own tiled gate: per-row relative L2 within 5e-3
+    # (tests/paged_attention_reference.py:68).
     p = _reference_test_inputs()
     for tile in (2, 3, 5, 16):
         a = orc.bf16_to_f32(orc.tiled_bf16_pv(p, tile)).astype(np.float64)
