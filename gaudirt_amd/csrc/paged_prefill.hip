@@ -77,6 +77,7 @@ struct PrefillArgs {
   int32_t window;
   uint16_t* out;
   int64_t out_stride;
+  DivMagic tiles_div, seqs_div, group_div;  // division by tiles, seqs and group (work_order.hpp)
 };
 
 template <int D>
@@ -112,12 +113,15 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // kStages K/V stages. The direct loads are asm statements the compiler does
   // not track, so one array serves every stage; reads are ordered by the
   // explicit vmcnt wait and the barrier of each step.
-  // The same LDS holds, after the step loop, each wave's output rows in bf16
-  // (rows padded by 16 bytes so that the four q-groups' rows of a write fall
-  // on different banks), read back as 16-byte pieces for the global stores.
+  // A region of its own (after the stages) holds, after the step loop, each
+  // wave's output rows in bf16 (rows padded by 16 bytes so that the four
+  // q-groups' rows of a write fall on different banks), read back as 16-byte
+  // pieces for the global stores. Being separate from the stages, a wave
+  // starts its output as soon as its own last step ends, with no barrier
+  // (132 KiB at head_dim 128, one workgroup per CU either way).
   constexpr int kOutRowBytes = 2 * D + 16;
   constexpr int kKvBytes = kStages * 2 * S::TILE, kOutBytes = kPrefillWaves * kQrowsPerWave * kOutRowBytes;
-  __shared__ __attribute__((aligned(16))) char lds[kKvBytes > kOutBytes ? kKvBytes : kOutBytes];
+  __shared__ __attribute__((aligned(16))) char lds[kKvBytes + kOutBytes];
   auto kv = reinterpret_cast<char(*)[2][S::TILE]>(lds);
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -129,17 +133,36 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // kv head's K/V (every row tile of every sequence, which share the prefix)
   // run under one L2 instead of fetching it into all eight. Inside its share
   // an XCD takes the row tiles highest first (heavy_first_item).
+  //
+  // The prologue is a chain of scalar loads: the arguments, the sequence's
+  // fields, its first block-table entry, then the first K/V tile. Each link is
+  // a memory round trip, so every argument is materialised in one batch at the
+  // top and the four sequence fields are loaded together ahead of the
+  // early-exit test (the compiler would otherwise fetch the sequence pointers
+  // after the work-item arithmetic and the fields one by one: six round trips
+  // before the first K/V load instead of three).
+  asm volatile("" ::"s"(a.seq_rows), "s"(a.seq_prefix), "s"(a.seq_first_row), "s"(a.seq_request),
+               "s"(a.block_tables), "s"(a.query), "s"(a.pool), "s"(a.out), "s"(a.tiles), "s"(a.seqs),
+               "s"(a.rows_per_tile), "s"(a.group), "s"(a.bt_stride), "s"(a.block_shift), "s"(a.window),
+               "s"(a.q_stride), "s"(a.slots), "s"(a.kv_heads), "s"(gridDim.x), "s"(a.tiles_div.mul),
+               "s"(a.tiles_div.shift), "s"(a.seqs_div.mul), "s"(a.seqs_div.shift), "s"(a.group_div.mul),
+               "s"(a.group_div.shift));
   const int nitems = gridDim.x, xcd = blockIdx.x % kXcds, per_xcd = nitems / kXcds, extra = nitems % kXcds;
+  // Divisions by runtime values go through the host's multiply-shift pairs.
+  const auto div_tiles = [&](int x) { return (int)fast_div((uint32_t)x, a.tiles_div); };
+  const auto div_group = [&](int x) { return (int)fast_div((uint32_t)x, a.group_div); };
   const int item = heavy_first_item(xcd * per_xcd + min(xcd, extra), per_xcd + (xcd < extra), a.tiles,
-                                    (int)blockIdx.x / kXcds);
-  const int tile = item % a.tiles, seq = (item / a.tiles) % a.seqs, kvh = item / (a.tiles * a.seqs);
-  const int rows = a.seq_rows[seq];
+                                    (int)blockIdx.x / kXcds, div_tiles);
+  const int item_seq = div_tiles(item), tile = item - item_seq * a.tiles;
+  const int kvh = (int)fast_div((uint32_t)item_seq, a.seqs_div), seq = item_seq - kvh * a.seqs;
+  const int rows = a.seq_rows[seq], prefix = a.seq_prefix[seq], seq_first = a.seq_first_row[seq];
+  const int request = a.seq_request[seq];
+  asm volatile("" ::"s"(rows), "s"(prefix), "s"(seq_first), "s"(request));
   const int r0 = tile * a.rows_per_tile;
   if (r0 >= rows) return;
   const int nr = min(a.rows_per_tile, rows - r0);
-  const int prefix = a.seq_prefix[seq];
-  const int first_row = a.seq_first_row[seq] + r0;
-  const int32_t* __restrict__ bt = a.block_tables + (int64_t)a.seq_request[seq] * a.bt_stride;
+  const int first_row = seq_first + r0;
+  const int32_t* __restrict__ bt = a.block_tables + (int64_t)request * a.bt_stride;
   const int g = a.group;
   const int pos_lo = prefix + r0, pos_hi = prefix + r0 + nr - 1;
   const int key_end = pos_hi + 1;
@@ -154,7 +177,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
     const int qr = wave * kQrowsPerWave + nt * 16 + c16;
-    const int row = qr / g, head = qr % g;
+    const int row = div_group(qr), head = qr - row * g;
     qvalid[nt] = row < nr;
     qpos[nt] = qvalid[nt] ? pos_lo + row : -1;
     qleft[nt] = a.window > 0 ? qpos[nt] - a.window + 1 : 0;
@@ -168,9 +191,9 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   }
 
   // Smallest query position and largest window start over this wave's valid rows.
-  const int wave_pos_min = pos_lo + (wave * kQrowsPerWave) / g;
+  const int wave_pos_min = pos_lo + div_group(wave * kQrowsPerWave);
   const int wave_left_max =
-      a.window > 0 ? pos_lo + min(nr - 1, (wave * kQrowsPerWave + kQrowsPerWave - 1) / g) - a.window + 1 : 0;
+      a.window > 0 ? pos_lo + min(nr - 1, div_group(wave * kQrowsPerWave + kQrowsPerWave - 1)) - a.window + 1 : 0;
 
   // At d 128 the row sums of the bf16 probabilities run on one more MFMA per
   // half step against an all-ones operand, in the output layout (rows 4q + r).
@@ -552,8 +575,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // wave's LDS operations complete in order, so it reads back what it wrote.
   // (Stored straight from the MFMA layout, a lane's values are 2-byte
   // elements 32 bytes apart: 64 narrow stores per lane.)
-  __syncthreads();  // every wave has finished reading the K/V stages
-  char* rows_lds = lds + wave * kQrowsPerWave * kOutRowBytes;
+  char* rows_lds = lds + kKvBytes + wave * kQrowsPerWave * kOutRowBytes;
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
     float l = 0.f;
@@ -574,7 +596,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   for (int i = 0; i < kPieces / 64; ++i) {
     const int piece = i * 64 + lane, ql = piece / (D / 8), part = piece % (D / 8);
     const int qr = wave * kQrowsPerWave + ql;
-    const int row = qr / g, head = qr % g;
+    const int row = div_group(qr), head = qr - row * g;
     const uint4 v = *reinterpret_cast<const uint4*>(rows_lds + ql * kOutRowBytes + part * 16);
     if (row < nr)
       *reinterpret_cast<uint4*>(a.out + (int64_t)(first_row + row) * a.out_stride + (int64_t)(kvh * g + head) * D +
@@ -647,6 +669,9 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
   a.window = p->sliding_window > 0 ? p->sliding_window : 0;
   a.out = static_cast<uint16_t*>(p->out);
   a.out_stride = p->out_row_stride;
+  a.tiles_div = div_magic((uint32_t)a.tiles);
+  a.seqs_div = div_magic((uint32_t)a.seqs);
+  a.group_div = div_magic((uint32_t)a.group);
   const int64_t items = (int64_t)a.tiles * p->kv_heads * p->seqs;
   if (items > (int64_t)1 << 30) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: too many rows");
   const dim3 grid((unsigned)items);

@@ -3,7 +3,28 @@
 // device code, and the CPU tests compile it with g++.
 #pragma once
 
+#include <cstdint>
+
 namespace gk {
+
+// Division by a runtime divisor 1 <= d <= 2^31 as a multiply and a shift, for
+// dividends 0 <= x < 2^31: with s = ceil(log2 d), mul = floor(2^(31+s) / d) + 1
+// (below 2^32) and shift = 31 + s, x / d == (x * mul) >> shift, because
+// x * mul / 2^(31+s) exceeds x / d by less than 2^-s <= 1/d. The host computes
+// the pair once per launch; a kernel then divides in two or three
+// instructions instead of the ~25 of a general 32-bit division.
+struct DivMagic {
+  uint32_t mul, shift;
+};
+
+constexpr DivMagic div_magic(uint32_t d) {
+  uint32_t s = 0;
+  while (s < 32 && (uint64_t(1) << s) < d) ++s;
+  return DivMagic{uint32_t((uint64_t(1) << (31 + s)) / d + 1), 31 + s};
+}
+
+constexpr uint32_t fast_div(uint32_t x, DivMagic m) { return uint32_t((uint64_t(x) * m.mul) >> m.shift); }
+
 
 // The j-th item (0 <= j < cnt) of an XCD whose share is the items
 // [lo, lo + cnt) of a launch ordered (kv head, sequence, row tile), row tiles
@@ -14,30 +35,40 @@ namespace gk {
 // behind the heavy ones (longest processing time first): with two rounds of
 // workgroups per CU the heaviest tile is paired with the lightest instead of
 // with another heavy one.
-constexpr int heavy_first_item(int lo, int cnt, int tiles, int j) {
+template <class DivTiles>
+constexpr int heavy_first_item(int lo, int cnt, int tiles, int j, DivTiles div_tiles) {
   // u = tiles - 1 - tile ranks the tiles heaviest first. Tile t occurs `full`
   // times in the share, once more when (t - lo) mod tiles < rem: for u in
-  // [a0, b0) and in [a1, tiles).
-  const long long n = tiles, full = cnt / tiles, rem = cnt % tiles, r0 = lo % tiles;
-  const long long b0 = n - r0;
-  const long long a0 = b0 - rem > 0 ? b0 - rem : 0;
-  const long long a1 = 2 * n - r0 - rem > b0 ? 2 * n - r0 - rem : b0;
-  // Items of the share whose rank is below u.
-  auto below = [&](long long u) {
-    long long e0 = u - a0, e1 = u - a1;
+  // [a0, b0) and in [a1, tiles). 32-bit arithmetic (the kernel runs this on
+  // the scalar unit, where 64-bit division costs hundreds of instructions):
+  // with lo + cnt <= 2^30 every value stays below 2^31; a1 is capped at n,
+  // which leaves below() unchanged for the ranks u < n it is asked about.
+  const int n = tiles, full = div_tiles(cnt), rem = cnt - full * n, r0 = lo - div_tiles(lo) * n;
+  const int b0 = n - r0;
+  const int a0 = b0 - rem > 0 ? b0 - rem : 0;
+  const int x = n - r0 - rem;  // a1 = max(x + n, b0), capped at n
+  const int a1 = x >= 0 ? n : (x + n > b0 ? x + n : b0);
+  // Items of the share whose rank is below u (at most cnt).
+  auto below = [&](int u) {
+    int e0 = u - a0, e1 = u - a1;
     e0 = e0 < 0 ? 0 : (e0 > b0 - a0 ? b0 - a0 : e0);
     e1 = e1 < 0 ? 0 : e1;
     return full * u + e0 + e1;
   };
   // Largest rank u with below(u) <= j; its tile holds item j.
-  long long lo_u = 0, hi_u = n - 1;
+  int lo_u = 0, hi_u = n - 1;
   while (lo_u < hi_u) {
-    const long long mid = (lo_u + hi_u + 1) / 2;
+    const int mid = (lo_u + hi_u + 1) / 2;
     if (below(mid) <= j) lo_u = mid;
     else hi_u = mid - 1;
   }
-  const long long tile = n - 1 - lo_u, k = j - below(lo_u);
-  return (int)(lo + (tile - r0 + n) % n + k * n);
+  const int tile = n - 1 - lo_u, k = j - below(lo_u);
+  const int t = tile - r0 + n;  // in [1, 2n)
+  return lo + (t >= n ? t - n : t) + k * n;
+}
+
+constexpr int heavy_first_item(int lo, int cnt, int tiles, int j) {
+  return heavy_first_item(lo, cnt, tiles, j, [tiles](int x) { return x / tiles; });
 }
 
 }  // namespace gk
