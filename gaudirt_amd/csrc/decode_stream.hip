@@ -33,6 +33,7 @@
 // to bf16, P . V from a transposed LDS read, both tiles loaded HBM -> LDS with
 // 16-byte buffer loads (global_load_lds_dwordx4).
 #include "decode_common.hpp"
+#include "work_order.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -47,6 +48,7 @@ struct StreamArgs {
   DecodeArgs d;
   int32_t units_per_row;  // kv_heads * head_groups
   int32_t wgs;            // workgroups of the grid
+  DivMagic wgs_div, head_groups_div, kv_heads_div;  // division by wgs, head_groups, kv_heads (work_order.hpp)
   float* unit_span;       // per unit: {first partial slot, last workgroup} as int32 bits
 };
 
@@ -67,22 +69,21 @@ __device__ __forceinline__ RowTiles row_tiles(int ctx, int window) {
 }
 
 
-__device__ __forceinline__ int bperm(int lane_src, int x) { return __builtin_amdgcn_ds_bpermute(lane_src << 2, x); }
-
-__device__ __forceinline__ int wave_sum(int x, int lane) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) x += bperm(lane ^ m, x);
-  return __builtin_amdgcn_readfirstlane(x);
-}
-
-__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = bperm(lane - d, x);
-    if (lane >= d) x += y;
-  }
+// Inclusive prefix sum over the wave's 64 lanes with DPP lane shifts (no LDS
+// round trips): row_shr 1, 2, 4, 8 scan each 16-lane row (a source outside
+// the row reads 0), then row_bcast:15 adds row 0's total into row 1 and row
+// 2's into row 3, and row_bcast:31 adds the total of rows 0-1 into rows 2-3.
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
   return x;
 }
+
+__device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlane(wave_inclusive_scan(x), 63); }
 
 // Position in the tile sequence, with the row data it needs (wave-uniform).
 struct Cursor {
@@ -181,13 +182,17 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 #pragma unroll
   for (int k = 0; k < kPre; ++k)
     if (64 * k + lane < a.rows) lane_tiles += row_tiles<TS>(pctx[k], a.window).count;
-  int64_t total = wave_sum(lane_tiles, lane);
+  int64_t total = wave_sum(lane_tiles);
   for (int base = 64 * kPre; base < a.rows; base += 64) {
     const int r = base + lane;
-    total += wave_sum(r < a.rows ? row_tiles<TS>(a.row_context[r], a.window).count : 0, lane);
+    total += wave_sum(r < a.rows ? row_tiles<TS>(a.row_context[r], a.window).count : 0);
   }
   total *= U;
-  const int64_t per = (total + sa.wgs - 1) / sa.wgs;
+  // Divisions on the scalar unit: 32-bit multiply-shift forms whenever the
+  // dividend allows (always at realistic sizes), 64-bit division otherwise.
+  const int64_t per = total + sa.wgs - 1 < (int64_t(1) << 31)
+                          ? (int64_t)fast_div((uint32_t)(total + sa.wgs - 1), sa.wgs_div)
+                          : (total + sa.wgs - 1) / sa.wgs;
   const int64_t g_begin = (int64_t)w * per;
   const int64_t g_end = min(g_begin + per, total);
   if (g_begin >= g_end) return;
@@ -202,7 +207,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     if (found || 64 * k >= a.rows) continue;
     const int r = 64 * k + lane;
     const int n = r < a.rows ? row_tiles<TS>(pctx[k], a.window).count : 0;
-    const int incl = wave_inclusive_scan(n, lane);
+    const int incl = wave_inclusive_scan(n);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(r < a.rows && (pre + incl) * U > g_begin);
     if (hit) {
       const int f = __builtin_ctzll(hit);
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     load_window(base);
     const int r = base + lane;
     const int n = r < a.rows ? row_tiles<TS>(wctx, a.window).count : 0;
-    const int incl = wave_inclusive_scan(n, lane);
+    const int incl = wave_inclusive_scan(n);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(r < a.rows && (pre + incl) * U > g_begin);
     if (hit) {
       const int f = __builtin_ctzll(hit);
@@ -233,8 +238,10 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 
   // A new unit's kv head and the rotation of its tile order.
   auto enter_unit = [&](Cursor& c) {
-    c.kvh = c.h / a.head_groups;
-    c.rot = (int)((int64_t)c.kvh * c.rt.count / a.kv_heads);
+    c.kvh = (int)fast_div((uint32_t)c.h, sa.head_groups_div);
+    const int64_t spread = (int64_t)c.kvh * c.rt.count;
+    c.rot = spread < (int64_t(1) << 31) ? (int)fast_div((uint32_t)spread, sa.kv_heads_div)
+                                         : (int)(spread / a.kv_heads);
   };
   Cursor cur;
   {
@@ -243,8 +250,8 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     cur.rt = row_tiles<TS>(__builtin_amdgcn_readlane(wctx, l), a.window);
     cur.req = __builtin_amdgcn_readlane(wreq, l);
     cur.qrow = __builtin_amdgcn_readlane(wmap, l);
-    const int64_t off = g_begin - row_base;
-    cur.h = (int)(off / cur.rt.count);
+    const int64_t off = g_begin - row_base;  // below U * count
+    cur.h = off < (int64_t(1) << 31) ? (int)((uint32_t)off / (uint32_t)cur.rt.count) : (int)(off / cur.rt.count);
     cur.j = (int)(off - (int64_t)cur.h * cur.rt.count);
     cur.g = g_begin;
     enter_unit(cur);
@@ -836,6 +843,9 @@ int launch_stream_decode(const DecodeArgs& a, bool softcap, int head_dim, int wg
   sa.d = a;
   sa.units_per_row = a.kv_heads * a.head_groups;
   sa.wgs = wgs;
+  sa.wgs_div = div_magic((uint32_t)wgs);
+  sa.head_groups_div = div_magic((uint32_t)a.head_groups);
+  sa.kv_heads_div = div_magic((uint32_t)a.kv_heads);
   const size_t parts = (size_t)2 * wgs * a.heads_per_group;
   const size_t o_bytes = (parts * head_dim * sizeof(float) + 255) & ~size_t{255};
   const size_t ml_bytes = (parts * 2 * sizeof(float) + 255) & ~size_t{255};
