@@ -580,11 +580,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   for (int nt = 0; nt < kNT; ++nt) {
     float l = 0.f;
     if constexpr (!kMfmaSum) l = col4_sum(l_run[nt][0]);
+    // The hardware reciprocal (within one fp32 ulp, far below the bf16
+    // rounding that follows) instead of a full division; every row sum is at
+    // least 1 (the row's maximum contributes at least 1).
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float lr = kMfmaSum ? l_run[nt][r]
                                 : __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l)));
-      const float inv = lr > 0.f ? 1.f / lr : 0.f;
+      const float inv = lr > 0.f ? __builtin_amdgcn_rcpf(lr) : 0.f;
       __bf16* dst = reinterpret_cast<__bf16*>(rows_lds + (nt * 16 + 4 * q + r) * kOutRowBytes) + c16;
 #pragma unroll
       for (int c = 0; c < S::NO; ++c) dst[16 * c] = (__bf16)(o[nt][c][r] * inv);
