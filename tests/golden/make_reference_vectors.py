@@ -16,9 +16,13 @@ Cases:
            block 128); kv tiles 512 (the reference harness's tile) and 64.
   prefill  tests/paged_cases.PrefillCase(31, 14, 2, 64, 16, prefixes=[300, 0], chunks=[9, 7])
            (the reference's multi-tile geometry, 14 q / 2 kv heads, d 64), kv tiles 512 and 64.
+  long     the reference's multi-tile geometry at its first long case
+           (tests/multitile_paged_attention_unit_test.cpp:1642-1655: 3840 + 263): 14 q / 2 kv heads,
+           d 64, block 16, inputs from tests/paged_cases.PrefillCase(47, ...); outputs of the rows
+           at every 32-row boundary (long_rows) only, to keep the file small.
   round    direct_bf16 on edge values (ties, the bf16 subnormal range, overflow) and on
            seeded random doubles over the whole exponent range.
-The c1 and prefill inputs are regenerated from their seeds by the tests; a SHA-256
+The c1, prefill and long inputs are regenerated from their seeds by the tests; a SHA-256
 of their bits is stored to catch a generator that drifts.
 
 Run from the repository root, in a container that holds the reference checkout:
@@ -35,6 +39,9 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 ROOT = pathlib.Path(__file__).resolve().parents[2]
+# Rows of the long case kept: both sides of every 32-row boundary, and the last row.
+LONG_ROWS = np.array(sorted({r for k in range(0, 263, 32) for r in (k - 1, k) if 0 <= r < 263} | {262}),
+                     dtype=np.int64)
 OUT = pathlib.Path(__file__).resolve().parent / "reference_vectors.npz"
 
 
@@ -123,6 +130,16 @@ def main():
     out["prefill_direct"] = bits(direct_bf16_pv(*a))
     for tile in (512, 64):
         out[f"prefill_tiled_{tile}"] = bits(tiled_bf16_pv(*a, tile))
+
+    # long: 3840-token prefix + 263 rows, rows at the 32-row boundaries
+    lc = cases.PrefillCase(47, 14, 2, 64, 16, prefixes=[3840], chunks=[263])
+    out["long_input_sha256"] = np.array(digest(lc.query, lc.pool, lc.block_tables))
+    rows = LONG_ROWS
+    out["long_rows"] = rows
+    a = reference_args(lc, lc.requests, lc.positions)
+    a = (a[0][rows],) + a[1:3] + (a[3][rows], a[4][rows]) + a[5:]
+    out["long_direct"] = bits(direct_bf16_pv(*a))
+    out["long_tiled_512"] = bits(tiled_bf16_pv(*a, 512))
 
     # round: direct fp64 -> bf16
     values64 = rounding_inputs()

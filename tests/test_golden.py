@@ -5,9 +5,11 @@ direct_bf16_pv and tiled_bf16_pv (tests/paged_attention_reference.py:6-59),
 direct_tiled (tests/paged_attention_reference_test.py:8-28) and direct_bf16
 (tests/fp64_reference.py:7-29), written by tests/golden/make_reference_vectors.py.
 Where the oracle's fp32 arithmetic and torch's (its vectorised exp, its
-reduction order) round one probability to a different bf16 value, an output
-moves by at most that probability's ulp times |v|; such elements are counted
-and bounded, everything else must match bit for bit.
+reduction order) round one probability, or an output's fp32 sum, to a
+different value, an output moves by about one bf16 step of a probability
+times |v|: such elements are counted and bounded (max-abs 2e-3, mean-abs 2e-6
+over the output, a thousandth of the parity gate's mean); the cases the
+reference's own tests use match bit for bit.
 """
 
 import hashlib
@@ -21,7 +23,7 @@ from tests import paged_cases as cases
 
 GOLDEN = pathlib.Path(__file__).resolve().parent / "golden" / "reference_vectors.npz"
 # A probability rounding flip moves an output by about 2^-9 * p * |v| <= ~1e-3 at these sizes.
-FLIP_ABS, FLIP_FRACTION = 2e-3, 0.005
+FLIP_ABS, FLIP_MEAN = 2e-3, 2e-6
 
 
 @pytest.fixture(scope="module")
@@ -41,11 +43,12 @@ def compare(name, mine, ref, exact=False):
     assert mine.shape == ref.shape and mine.dtype == ref.dtype == np.uint16
     diff = np.abs(orc.bf16_to_f32(mine).astype(np.float64) - orc.bf16_to_f32(ref).astype(np.float64))
     flips = int((mine != ref).sum())
-    print(f"{name}: {flips} of {mine.size} elements differ, max_abs={diff.max():.3e}", flush=True)
+    print(f"{name}: {flips} of {mine.size} elements differ, max_abs={diff.max():.3e} mean_abs={diff.mean():.2e}",
+          flush=True)
     if exact:
         assert flips == 0, name
     else:
-        assert diff.max() <= FLIP_ABS and flips <= FLIP_FRACTION * mine.size, name
+        assert diff.max() <= FLIP_ABS and diff.mean() <= FLIP_MEAN, name
 
 
 def reftest_problem(g):
@@ -99,9 +102,24 @@ def test_prefill_chunk(golden):
     compare("prefill tiled_bf16_pv 64", orc.tiled_bf16_pv(p, 64), golden["prefill_tiled_64"])
 
 
+def test_long_prefill_rows(golden):
+    # A 3840-token prefix and 263 chunk rows: many 512-key tiles per row, the rows
+    # on both sides of every 32-row boundary.
+    lc = golden_long_case()
+    assert digest(lc.query, lc.pool, lc.block_tables) == str(golden["long_input_sha256"])
+    p = lc.oracle_problem(rows=golden["long_rows"])
+    compare("long direct_bf16_pv", orc.direct_bf16_pv(p), golden["long_direct"])
+    compare("long tiled_bf16_pv 512", orc.tiled_bf16_pv(p, 512), golden["long_tiled_512"])
+
+
 def test_fp64_to_bf16_rounding_bit_exact(golden):
     mine = orc.bf16_from_f64(golden["round_inputs"])
     assert np.array_equal(mine, golden["round_bits"])
+
+
+def golden_long_case():
+    """The long case of the vectors: 14 q / 2 kv heads, d 64, block 16, a 3840-token prefix + 263 rows."""
+    return cases.PrefillCase(47, 14, 2, 64, 16, prefixes=[3840], chunks=[263])
 
 
 def golden_prefill_case():

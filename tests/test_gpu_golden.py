@@ -12,7 +12,7 @@ import pytest
 
 from oracle import oracle as orc
 from tests import paged_cases as cases
-from tests.test_golden import GOLDEN, golden_prefill_case
+from tests.test_golden import GOLDEN, golden_long_case, golden_prefill_case
 
 pytestmark = pytest.mark.gpu
 
@@ -50,4 +50,10 @@ def test_c1_decode_against_reference_vectors(runner, golden, partition):
 def test_prefill_against_reference_vectors(runner, golden):
     actual = runner.run_prefill_case(golden_prefill_case())
     for name in ("prefill_direct", "prefill_tiled_512", "prefill_tiled_64"):
+        gate(f"vs {name}", actual, golden[name])
+
+
+def test_long_prefill_against_reference_vectors(runner, golden):
+    actual = runner.run_prefill_case(golden_long_case())[golden["long_rows"]]
+    for name in ("long_direct", "long_tiled_512"):
         gate(f"vs {name}", actual, golden[name])
