@@ -15,8 +15,9 @@ written by tests/golden/make_reference_vectors.py from tests/paged_attention_ref
 tests/paged_attention_reference_test.py and tests/fp64_reference.py; checked by
 tests/test_golden.py) pin ``direct_bf16_pv``, ``tiled_bf16_pv``, ``direct_tiled`` and
 ``bf16_from_f64`` bit for bit on the reference test's inputs, the C1 case and 2,224
-roundings; on a d 64 chunked-prefill case 15 of 14,336 outputs differ where torch's
-fp32 exp rounds one probability to the neighbouring bf16 value (max abs 9.8e-4).
+roundings; on d 64 chunked-prefill cases (a 300-token prefix; the reference's 3840 + 263
+multi-tile shape) a few outputs differ where torch's fp32 exp or summation order rounds a
+probability or a sum differently (max abs 9.8e-4, mean abs at most 6e-7).
 
 - ``bf16_from_f64``: the known answer of tests/decoder_cpu_reference_test.py:66-68
   (1 + 2^-8 + 2^-32 -> 1 + 2^-7), exact rational rounding with ``fractions`` on
