@@ -20,9 +20,11 @@ Cases:
            (tests/multitile_paged_attention_unit_test.cpp:1642-1655: 3840 + 263): 14 q / 2 kv heads,
            d 64, block 16, inputs from tests/paged_cases.PrefillCase(47, ...); outputs of the rows
            at every 32-row boundary (long_rows) only, to keep the file small.
+  decode_long  decode rows at C5's group (16 q / 2 kv heads, d 128, block 128) with contexts
+           32768, 20000 and 777: tests/paged_cases.decode_case(53, ...); kv tile 512.
   round    direct_bf16 on edge values (ties, the bf16 subnormal range, overflow) and on
            seeded random doubles over the whole exponent range.
-The c1, prefill and long inputs are regenerated from their seeds by the tests; a SHA-256
+The c1, prefill, long and decode_long inputs are regenerated from their seeds by the tests; a SHA-256
 of their bits is stored to catch a generator that drifts.
 
 Run from the repository root, in a container that holds the reference checkout:
@@ -140,6 +142,13 @@ def main():
     a = (a[0][rows],) + a[1:3] + (a[3][rows], a[4][rows]) + a[5:]
     out["long_direct"] = bits(direct_bf16_pv(*a))
     out["long_tiled_512"] = bits(tiled_bf16_pv(*a, 512))
+
+    # decode_long: one row at 32768 keys, split over many workgroups by the balanced decode
+    dl = cases.decode_case(53, 3, 16, 2, 128, 128, 420, [32768, 20000, 777])
+    out["decode_long_input_sha256"] = np.array(digest(dl.query, dl.pool, dl.block_tables, dl.lens))
+    a = reference_args(dl, np.arange(dl.batch), dl.lens.astype(np.int64) - 1)
+    out["decode_long_direct"] = bits(direct_bf16_pv(*a))
+    out["decode_long_tiled_512"] = bits(tiled_bf16_pv(*a, 512))
 
     # round: direct fp64 -> bf16
     values64 = rounding_inputs()

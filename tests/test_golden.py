@@ -112,9 +112,23 @@ def test_long_prefill_rows(golden):
     compare("long tiled_bf16_pv 512", orc.tiled_bf16_pv(p, 512), golden["long_tiled_512"])
 
 
+def test_long_decode(golden):
+    # C5's group at contexts up to 32768 keys.
+    dl = golden_long_decode_case()
+    assert digest(dl.query, dl.pool, dl.block_tables, dl.lens) == str(golden["decode_long_input_sha256"])
+    p = dl.oracle_problem()
+    compare("long decode direct_bf16_pv", orc.direct_bf16_pv(p), golden["decode_long_direct"])
+    compare("long decode tiled_bf16_pv 512", orc.tiled_bf16_pv(p, 512), golden["decode_long_tiled_512"])
+
+
 def test_fp64_to_bf16_rounding_bit_exact(golden):
     mine = orc.bf16_from_f64(golden["round_inputs"])
     assert np.array_equal(mine, golden["round_bits"])
+
+
+def golden_long_decode_case():
+    """The long decode case of the vectors: 16 q / 2 kv heads, d 128, block 128, contexts 32768, 20000, 777."""
+    return cases.decode_case(53, 3, 16, 2, 128, 128, 420, [32768, 20000, 777])
 
 
 def golden_long_case():

@@ -12,7 +12,7 @@ import pytest
 
 from oracle import oracle as orc
 from tests import paged_cases as cases
-from tests.test_golden import GOLDEN, golden_long_case, golden_prefill_case
+from tests.test_golden import GOLDEN, golden_long_case, golden_long_decode_case, golden_prefill_case
 
 pytestmark = pytest.mark.gpu
 
@@ -57,3 +57,10 @@ def test_long_prefill_against_reference_vectors(runner, golden):
     actual = runner.run_prefill_case(golden_long_case())[golden["long_rows"]]
     for name in ("long_direct", "long_tiled_512"):
         gate(f"vs {name}", actual, golden[name])
+
+
+@pytest.mark.parametrize("partition", [0, 2048])
+def test_long_decode_against_reference_vectors(runner, golden, partition):
+    actual = runner.run_case(golden_long_decode_case(), partition=partition)
+    for name in ("decode_long_direct", "decode_long_tiled_512"):
+        gate(f"partition {partition} vs {name}", actual, golden[name])
