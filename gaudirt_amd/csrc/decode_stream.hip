@@ -91,7 +91,7 @@ struct Cursor {
   int kvh, rot;             // the unit's kv head; rotation of its tile order
   RowTiles rt;
   int req, qrow;            // block-table row, query/output row
-  int64_t g;                // index in the tile sequence
+  int g;                    // index in the tile sequence (below 2^31: the host routes larger batches elsewhere)
   int next_ctx, next_req, next_qrow;  // row + 1, fetched ahead
 };
 
@@ -105,7 +105,7 @@ struct TileDesc {
   int tb;                   // first key of the tile
   int left, ctx;            // visible keys of the row
   int row, h, kvh, j, count, qrow;
-  int64_t g;
+  int g;
   uint32_t row0[NR];        // byte offset of run i's first key in its kv head's K (and V) region
   int q_start, q_end;       // first / last tile of the unit in this workgroup
 };
@@ -188,19 +188,19 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     total += wave_sum(r < a.rows ? row_tiles<TS>(a.row_context[r], a.window).count : 0);
   }
   total *= U;
-  // Divisions on the scalar unit: 32-bit multiply-shift forms whenever the
-  // dividend allows (always at realistic sizes), 64-bit division otherwise.
-  const int64_t per = total + sa.wgs - 1 < (int64_t(1) << 31)
-                          ? (int64_t)fast_div((uint32_t)(total + sa.wgs - 1), sa.wgs_div)
-                          : (total + sa.wgs - 1) / sa.wgs;
-  const int64_t g_begin = (int64_t)w * per;
-  const int64_t g_end = min(g_begin + per, total);
+  // The tile sequence is numbered in 32 bits from here on (fewer scalar
+  // registers in the tile loop): the host sends only batches whose tiles,
+  // with row_context <= max_context, stay below 2^31.
+  if (total + sa.wgs >= (int64_t(1) << 31)) return;
+  const int per = (int)fast_div((uint32_t)(total + sa.wgs - 1), sa.wgs_div);
+  const int g_begin = w * per;
+  const int g_end = min(g_begin + per, (int)total);
   if (g_begin >= g_end) return;
 
   // The row holding tile g_begin, and the sequence index of its first tile.
   int row = 0;
-  int64_t row_base = 0;
-  int64_t pre = 0;
+  int row_base = 0;
+  int pre = 0;
   bool found = false;
 #pragma unroll
   for (int k = 0; k < kPre; ++k) {
@@ -250,9 +250,9 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     cur.rt = row_tiles<TS>(__builtin_amdgcn_readlane(wctx, l), a.window);
     cur.req = __builtin_amdgcn_readlane(wreq, l);
     cur.qrow = __builtin_amdgcn_readlane(wmap, l);
-    const int64_t off = g_begin - row_base;  // below U * count
-    cur.h = off < (int64_t(1) << 31) ? (int)((uint32_t)off / (uint32_t)cur.rt.count) : (int)(off / cur.rt.count);
-    cur.j = (int)(off - (int64_t)cur.h * cur.rt.count);
+    const int off = g_begin - row_base;  // below U * count
+    cur.h = (int)((uint32_t)off / (uint32_t)cur.rt.count);
+    cur.j = off - cur.h * cur.rt.count;
     cur.g = g_begin;
     enter_unit(cur);
     cur.next_ctx = cur.next_req = cur.next_qrow = 0;
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     const int kvh = t.kvh, hg = t.h - kvh * a.head_groups;
     const int hv = min(16, a.group - hg * 16);
     const int head0 = kvh * a.group + hg * 16;
-    const int64_t g0 = t.g - t.j;  // the unit's first tile
+    const int g0 = t.g - t.j;  // the unit's first tile
     if (kMaxPend == 2 && npend == 2) {
       flush(pend0);
       pend0 = pend1;
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     e.span0 = e.span1 = 0;
     if (t.j == t.count - 1) {
       // This workgroup holds the unit's last tile: record where its partials are.
-      const int64_t wf = g0 / per;
+      const int wf = (int)((uint32_t)g0 / (uint32_t)per);
       e.span = sa.unit_span + ((int64_t)t.row * U + t.h) * 2;
       e.span0 = (int)(2 * wf + (g0 == wf * per ? 0 : 1));
       e.span1 = w;
@@ -633,7 +633,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 
   // ---- Pipeline ------------------------------------------------------------
   // Stage 0 / stage 1 alternate; the query buffer alternates per unit.
-  int64_t to_issue = g_end - g_begin;  // tiles not yet issued
+  int to_issue = g_end - g_begin;  // tiles not yet issued
   int qpar = 0;
   TileEntries<NR> first_entry = table_entry(cur);
   pack(first_entry);

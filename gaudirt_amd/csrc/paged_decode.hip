@@ -728,9 +728,16 @@ int device_cus() {
 // The balanced schedule (decode_stream.hip) serves the MFMA path, every block
 // size included, whenever the caller leaves the partition to the library; an
 // explicit partition and small groups take the partitioned kernels.
+// The balanced schedule numbers the batch's tiles in 32 bits: it runs when
+// every row's tiles (at most max_context / TS + 2 with a window's offset)
+// times the units fit below 2^31; larger batches take the partitioned kernel.
 bool use_stream(const gk_decode_params* p) {
   const int group = p->q_heads / p->kv_heads;
-  return p->partition_tokens == 0 && use_mfma(group);
+  if (p->partition_tokens != 0 || !use_mfma(group)) return false;
+  const int hpw = heads_per_workgroup(group);
+  const int64_t units = (int64_t)p->rows * p->kv_heads * ((group + hpw - 1) / hpw);
+  const int64_t ts = p->head_dim == 256 ? 16 : 32;
+  return units * ((int64_t)p->max_context / ts + 2) < (int64_t(1) << 31);
 }
 
 int32_t decode_partition(const gk_decode_params* p) {
