@@ -409,40 +409,45 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   // pipeline has drained (or when a third one needs the room). With D = 256
   // the registers are not there: segments are stored at once.
   constexpr int kMaxPend = D <= 128 ? 2 : 0;
+  // Indices and flags in 32-bit words, not pointers (fewer scalar registers
+  // held across the tile loop); addresses are formed when storing.
   struct Pending {
     f32x4_t v[S::NO];   // output rows already divided by l (output) or the raw partial
     float m, l;         // partial: running max / sum of head c16 (lanes q == 0)
-    float* dst;         // output row block (bf16) or partial block (fp32) of head 0
-    int hv;             // valid heads
-    int out;            // 1: bf16 output, 0: partial
-    float* span;        // unit_span entry to write (nullptr: none)
+    int dst;            // output row (bf16 output) or partial slot
+    int kind;           // valid heads | 32 for a bf16 output | head 0 << 6 (output)
+    int span;           // unit_span element of the record to write (-1: none)
     int span0, span1;
   };
   Pending pend0, pend1;
   int npend = 0;
   auto flush = [&](const Pending& e) {
+    const int hv = e.kind & 31;
+    const bool out = (e.kind & 32) != 0;
+    const int head0 = e.kind >> 6;
+    const int64_t part = (int64_t)e.dst * a.heads_per_group;  // partial slot's first head
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int h = 4 * q + r;
-      if (h >= e.hv) continue;
-      if (e.out) {
-        uint16_t* dst = reinterpret_cast<uint16_t*>(e.dst) + (int64_t)h * D + c16;
+      if (h >= hv) continue;
+      if (out) {
+        uint16_t* dst = a.out + (int64_t)e.dst * a.out_stride + (int64_t)(head0 + h) * D + c16;
 #pragma unroll
         for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(e.v[c][r]);
       } else {
-        float* dst = e.dst + (int64_t)h * D + c16;
+        float* dst = a.part_o + (part + h) * D + c16;
 #pragma unroll
         for (int c = 0; c < S::NO; ++c) dst[16 * c] = e.v[c][r];
       }
     }
-    if (!e.out && q == 0 && c16 < e.hv) {
-      float* ml = a.part_ml + (e.dst - a.part_o) / D * 2 + (int64_t)c16 * 2;
+    if (!out && q == 0 && c16 < hv) {
+      float* ml = a.part_ml + (part + c16) * 2;
       ml[0] = e.m;
       ml[1] = e.l;
     }
-    if (e.span && lane == 0) {
-      e.span[0] = __int_as_float(e.span0);
-      e.span[1] = __int_as_float(e.span1);
+    if (e.span >= 0 && lane == 0) {
+      sa.unit_span[e.span] = __int_as_float(e.span0);
+      sa.unit_span[e.span + 1] = __int_as_float(e.span1);
     }
   };
 
@@ -462,12 +467,11 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       npend = 1;
     }
     Pending e;
-    e.hv = hv;
     e.m = m_run;
     e.l = l_run;
     if (g0 >= g_begin && g0 + t.count <= g_end) {
-      e.out = 1;
-      e.dst = reinterpret_cast<float*>(a.out + (int64_t)t.qrow * a.out_stride + (int64_t)head0 * D);
+      e.kind = hv | 32 | (head0 << 6);
+      e.dst = t.qrow;
       float inv[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) inv[r] = lrow[r] > 0.f ? 1.f / lrow[r] : 0.f;
@@ -476,18 +480,17 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) e.v[c][r] = o[c][r] * inv[r];
     } else {
-      e.out = 0;
-      const int slot = 2 * w + (g0 <= g_begin ? 0 : 1);
-      e.dst = a.part_o + (int64_t)slot * a.heads_per_group * D;
+      e.kind = hv;
+      e.dst = 2 * w + (g0 <= g_begin ? 0 : 1);  // partial slot
 #pragma unroll
       for (int c = 0; c < S::NO; ++c) e.v[c] = o[c];
     }
-    e.span = nullptr;
+    e.span = -1;
     e.span0 = e.span1 = 0;
     if (t.j == t.count - 1) {
       // This workgroup holds the unit's last tile: record where its partials are.
       const int wf = (int)((uint32_t)g0 / (uint32_t)per);
-      e.span = sa.unit_span + ((int64_t)t.row * U + t.h) * 2;
+      e.span = (t.row * U + t.h) * 2;
       e.span0 = (int)(2 * wf + (g0 == wf * per ? 0 : 1));
       e.span1 = w;
     }
