@@ -104,11 +104,13 @@ template <int NR>
 struct TileDesc {
   int tb;                   // first key of the tile
   int left, ctx;            // visible keys of the row
-  int row, h, kvh, j, count, qrow;
+  int row, h, j, qrow;      // the unit (its kv head is h / head_groups) and the tile's place in it
   int g;
   uint32_t row0[NR];        // byte offset of run i's first key in its kv head's K (and V) region
-  int q_start, q_end;       // first / last tile of the unit in this workgroup
+  int flags;                // kTileFirst / kTileLast: first / last tile of the unit in this
+                            // workgroup; kUnitLast: the unit's last tile
 };
+constexpr int kTileFirst = 1, kTileLast = 2, kUnitLast = 4;
 
 // Block-table entries of one tile's runs.
 template <int NR>
@@ -315,6 +317,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     }
     return r;
   };
+  auto kv_head_of = [&](const TileDesc& t) { return (int)fast_div((uint32_t)t.h, sa.head_groups_div); };
   auto describe = [&](const Cursor& c, const TileEntries<NR>& en) {
     constexpr int NROW = MODE == kKeyBlocks ? 1 : NR;
     TileDesc t;
@@ -323,16 +326,14 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     t.ctx = c.rt.ctx;
     t.row = c.row;
     t.h = c.h;
-    t.kvh = c.kvh;
     t.j = c.j;
-    t.count = c.rt.count;
     t.qrow = c.qrow;
     t.g = c.g;
 #pragma unroll
     for (int i = 0; i < NROW; ++i)
       t.row0[i] = (((uint32_t)en.e[i] << shift) | (uint32_t)((t.tb + i * KPR) & block_mask)) * (uint32_t)(2 * D);
-    t.q_start = c.j == 0 || c.g == g_begin;
-    t.q_end = c.j == c.rt.count - 1 || c.g == g_end - 1;
+    t.flags = (c.j == 0 || c.g == g_begin ? kTileFirst : 0) |
+              (c.j == c.rt.count - 1 || c.g == g_end - 1 ? kTileLast : 0) | (c.j == c.rt.count - 1 ? kUnitLast : 0);
     return t;
   };
 
@@ -361,7 +362,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   };
   auto issue_tile = [&](const TileDesc& t, const TileEntries<NR>& en, char* kt, char* vt) {
     const int keyed = en.keyed;
-    const uint16_t* kbase = a.pool + (int64_t)t.kvh * a.slots * D;
+    const uint16_t* kbase = a.pool + (int64_t)kv_head_of(t) * a.slots * D;
     const uint16_t* vbase = kbase + (int64_t)a.kv_heads * a.slots * D;
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, region, kBufferDword3);
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, region, kBufferDword3);
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   // The unit's query heads -> LDS ([head][D], row-major). The resource covers
   // the valid heads only, so the rest of the buffer reads as zero.
   auto issue_query = [&](const TileDesc& t, char* qsb) {
-    const int kvh = t.kvh, hg = t.h - kvh * a.head_groups;
+    const int kvh = kv_head_of(t), hg = t.h - kvh * a.head_groups;
     const int hv = min(16, a.group - hg * 16);
     const uint16_t* qp = a.query + (int64_t)t.qrow * a.q_stride + (int64_t)(kvh * a.group + hg * 16) * D;
     const uint32_t bytes = (uint32_t)(hv * D * 2);
@@ -457,7 +458,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       lrow[r] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l_run)));
-    const int kvh = t.kvh, hg = t.h - kvh * a.head_groups;
+    const int kvh = kv_head_of(t), hg = t.h - kvh * a.head_groups;
     const int hv = min(16, a.group - hg * 16);
     const int head0 = kvh * a.group + hg * 16;
     const int g0 = t.g - t.j;  // the unit's first tile
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     Pending e;
     e.m = m_run;
     e.l = l_run;
-    if (g0 >= g_begin && g0 + t.count <= g_end) {
+    if (g0 >= g_begin && g0 + row_tiles<TS>(t.ctx, a.window).count <= g_end) {
       e.kind = hv | 32 | (head0 << 6);
       e.dst = t.qrow;
       float inv[4];
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     }
     e.span = -1;
     e.span0 = e.span1 = 0;
-    if (t.j == t.count - 1) {
+    if (t.flags & kUnitLast) {
       // This workgroup holds the unit's last tile: record where its partials are.
       const int wf = (int)((uint32_t)g0 / (uint32_t)per);
       e.span = (t.row * U + t.h) * 2;
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 
   // Attend one tile from one stage (its loads, and its unit's query, have landed).
   auto read_query = [&](const TileDesc& t, const char* qsb) {
-    const int hg = t.h - t.kvh * a.head_groups;
+    const int hg = t.h - kv_head_of(t) * a.head_groups;
     const int hv = min(16, a.group - hg * 16);
 #pragma unroll
     for (int c = 0; c < S::NC; ++c) {
@@ -514,7 +515,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     }
   };
   auto consume = [&](const TileDesc& t, const char* kt, char* vt, int qpar_t) {
-    if (t.q_start) {
+    if (t.flags & kTileFirst) {
       read_query(t, qs[qpar_t]);
 #pragma unroll
       for (int c = 0; c < S::NO; ++c) o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -631,7 +632,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     }
     // The stage is refilled next: every LDS read of it must have returned.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (t.q_end) finalize(t);
+    if (t.flags & kTileLast) finalize(t);
   };
 
   // ---- Pipeline ------------------------------------------------------------
@@ -642,7 +643,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   pack(first_entry);
   TileDesc d0 = describe(cur, first_entry), d1;
   int qp0 = 0, qp1 = 0;                // query buffer of the tile in stage 0 / 1
-  if (d0.q_start) issue_query(d0, qs[0]);
+  if (d0.flags & kTileFirst) issue_query(d0, qs[0]);
   issue_tile(d0, first_entry, kt0, vt0);
   --to_issue;
   TileEntries<NR> next_entry = {};
@@ -655,7 +656,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     bool more = to_issue > 0;
     if (more) {
       d1 = describe(cur, next_entry);
-      if (d1.q_start) {
+      if (d1.flags & kTileFirst) {
         qpar ^= 1;
         issue_query(d1, qs[qpar]);
       }
@@ -676,7 +677,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     more = to_issue > 0;
     if (more) {
       d0 = describe(cur, next_entry);
-      if (d0.q_start) {
+      if (d0.flags & kTileFirst) {
         qpar ^= 1;
         issue_query(d0, qs[qpar]);
       }
