@@ -2,6 +2,7 @@
 #pragma once
 
 #include "gk_mfma.hpp"
+#include "work_order.hpp"
 
 namespace gk {
 
@@ -29,11 +30,6 @@ struct DecodeArgs {
   float* part_o;
   float* part_ml;
 };
-
-// First visible key of a row of `ctx` keys under a sliding window (0 = none).
-__device__ __forceinline__ int visible_left(int ctx, int window) {
-  return (window > 0 && ctx > window) ? ctx - window : 0;
-}
 
 template <int D>
 struct MfmaShape {

@@ -64,7 +64,7 @@ __device__ __forceinline__ RowTiles row_tiles(int ctx, int window) {
   r.ctx = ctx > 0 ? ctx : 0;
   r.left = visible_left(r.ctx, window);
   r.first = r.left / TS;
-  r.count = r.ctx > 0 ? (r.ctx + TS - 1) / TS - r.first : 1;
+  r.count = stream_row_tile_count(r.ctx, window, TS);
   return r;
 }
 
@@ -192,8 +192,22 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   total *= U;
   // The tile sequence is numbered in 32 bits from here on (fewer scalar
   // registers in the tile loop): the host sends only batches whose tiles,
-  // with row_context <= max_context, stay below 2^31.
-  if (total + sa.wgs >= (int64_t(1) << 31)) return;
+  // with row_context <= max_context, stay below 2^31 (stream_tiles_fit). A
+  // caller whose row_context exceeds its max_context can still get here; then
+  // every output row becomes NaN and every span record is marked unwritten,
+  // so the merge leaves those rows alone instead of combining stale partials.
+  if (total + sa.wgs >= (int64_t(1) << 31)) {
+    for (int r = w; r < a.rows; r += sa.wgs) {
+      const int orow = a.row_map ? a.row_map[r] : r;
+      uint16_t* dst = a.out + (int64_t)orow * a.out_stride;
+      for (int e = lane; e < a.q_heads * D; e += 64) dst[e] = 0x7fc0;
+      for (int u = lane; u < U; u += 64) {
+        sa.unit_span[((int64_t)r * U + u) * 2] = __int_as_float(-1);
+        sa.unit_span[((int64_t)r * U + u) * 2 + 1] = __int_as_float(-1);
+      }
+    }
+    return;
+  }
   const int per = (int)fast_div((uint32_t)(total + sa.wgs - 1), sa.wgs_div);
   const int g_begin = w * per;
   const int g_end = min(g_begin + per, (int)total);

@@ -730,14 +730,16 @@ int device_cus() {
 // explicit partition and small groups take the partitioned kernels.
 // The balanced schedule numbers the batch's tiles in 32 bits: it runs when
 // every row's tiles (at most max_context / TS + 2 with a window's offset)
-// times the units fit below 2^31; larger batches take the partitioned kernel.
+// times the units, plus the grid's workgroups, stay below 2^31 (the kernel's
+// own test, stream_tiles_fit); larger batches take the partitioned kernel.
 bool use_stream(const gk_decode_params* p) {
   const int group = p->q_heads / p->kv_heads;
   if (p->partition_tokens != 0 || !use_mfma(group)) return false;
   const int hpw = heads_per_workgroup(group);
   const int64_t units = (int64_t)p->rows * p->kv_heads * ((group + hpw - 1) / hpw);
-  const int64_t ts = p->head_dim == 256 ? 16 : 32;
-  return units * ((int64_t)p->max_context / ts + 2) < (int64_t(1) << 31);
+  const int ts = p->head_dim == 256 ? 16 : 32;
+  return stream_tiles_fit(units, p->max_context, ts,
+                          stream_decode_wgs(p->head_dim, p->softcap > 0.f, p->block_size));
 }
 
 int32_t decode_partition(const gk_decode_params* p) {

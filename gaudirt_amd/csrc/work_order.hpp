@@ -71,4 +71,26 @@ constexpr int heavy_first_item(int lo, int cnt, int tiles, int j) {
   return heavy_first_item(lo, cnt, tiles, j, [tiles](int x) { return x / tiles; });
 }
 
+// First visible key of a row of `ctx` keys under a sliding window (0 = none).
+constexpr int visible_left(int ctx, int window) { return (window > 0 && ctx > window) ? ctx - window : 0; }
+
+// Tiles of one row in the balanced decode schedule: tile k holds the keys
+// [k ts, (k + 1) ts), and the row owns the tiles that hold its visible keys
+// [visible_left(ctx, window), ctx); an empty row owns one fully masked tile.
+// Without a window that is ceil(ctx / ts) <= ctx / ts + 1 tiles; a window can
+// start mid-tile, which adds at most one: never above ctx / ts + 2.
+constexpr int stream_row_tile_count(int ctx, int window, int ts) {
+  const int c = ctx > 0 ? ctx : 0;
+  return c > 0 ? (c + ts - 1) / ts - visible_left(c, window) / ts : 1;
+}
+
+// The balanced schedule numbers the tiles of a whole batch (units * tiles of
+// each row) in 32 bits, and its kernel splits them over `wgs` workgroups with
+// (total + wgs - 1) / wgs: total + wgs must stay below 2^31. With every
+// row_context <= max_context a row has at most max_context / ts + 2 tiles, so
+// the host runs the schedule only when this holds.
+constexpr bool stream_tiles_fit(int64_t units, int64_t max_context, int ts, int64_t wgs) {
+  return units >= 0 && max_context >= 0 && wgs >= 1 && units * (max_context / ts + 2) + wgs < (int64_t(1) << 31);
+}
+
 }  // namespace gk

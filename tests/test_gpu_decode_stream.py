@@ -288,3 +288,91 @@ def test_stream_graph_capture_matches_eager(runner):
         eager = runner.paged_decode(params)  # eager call between replays (default stream)
         torch.cuda.synchronize()
         del eager
+
+
+def _stream_grid_workgroups(lib, params):
+    """Workgroups of the balanced grid, read back from the workspace size the
+    library asks for: units * 8 bytes of span records plus, for head_dim 128 and
+    4 heads per workgroup, wgs * 4 * (128 * 4 * 2 + 2 * 4 * 2) bytes of partial
+    slots (both sections multiples of 256 bytes when 4 divides wgs)."""
+    import ctypes
+
+    units = params.rows * params.kv_heads
+    partial = lib.gk_paged_decode_workspace_bytes(ctypes.byref(params)) - units * 8
+    per_wg = 4 * (128 * 4 * 2 + 2 * 4 * 2)
+    assert partial > 0 and partial % per_wg == 0, partial
+    return partial // per_wg
+
+
+def test_stream_routing_boundary_includes_the_grid(runner):
+    # Host only (no launch): the balanced schedule numbers a batch's tiles in
+    # 32 bits, so gk_paged_decode takes it exactly while
+    # units * (max_context / 32 + 2) + workgroups < 2^31, and the partitioned
+    # kernel (a non-zero partition) from there on. The rows are chosen so that
+    # the workgroup term decides: without it the boundary would lie one tile
+    # per row later.
+    import ctypes
+    from gaudirt_amd import capi
+
+    lib = capi.load()
+    dummy = runner.to_device(np.zeros(16, dtype=np.int32))
+    params = capi.DecodeParams()
+    params.query = params.pool = params.out = dummy.data_ptr()
+    params.block_tables = params.row_context = dummy.data_ptr()
+    params.q_row_stride = params.out_row_stride = 32 * 128
+    params.slots, params.bt_stride, params.block_size = 1 << 20, 1, 128
+    params.q_heads, params.kv_heads, params.head_dim = 32, 8, 128
+    params.scale, params.softcap, params.sliding_window = 0.088, 0.0, -1
+    params.partition_tokens = 0
+    params.rows, params.max_context = 1, 64
+    wgs = _stream_grid_workgroups(lib, params)
+    print("balanced grid workgroups", wgs, flush=True)
+    limit = 1 << 31
+    checked = 0
+    for rows in range(65535, 0, -1):
+        units = rows * 8
+        n = (limit - 1) // units  # largest tile bound without the grid term
+        if units * n + wgs < limit or n < 3:
+            continue  # the grid term does not decide for this batch
+        params.rows = rows
+        params.max_context = (n - 2) * 32 - 1  # bound n - 1: fits with the grid term
+        assert units * (n - 1) + wgs < limit
+        assert lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0, (rows, params.max_context)
+        params.max_context = (n - 2) * 32  # bound n: fits only without the grid term
+        assert lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) != 0, (rows, params.max_context)
+        checked += 1
+        if checked == 3:
+            break
+    assert checked == 3
+
+
+def test_stream_contexts_beyond_max_context_give_nan_not_stale_output(runner):
+    # A caller that breaks the contract row_context <= max_context can make the
+    # balanced schedule's tile count reach 2^31 although the host routed the
+    # batch to it. The kernel then writes NaN into every output row and marks
+    # every span record unwritten, so the merge keeps the NaN; no key is read.
+    # A first call on the same workspace leaves valid span records behind.
+    import torch
+
+    rows, heads, kv_heads, d, block = 65535, 32, 8, 128, 128
+    ctx = 4097 * 32  # 65535 rows * 8 kv heads * 4097 tiles > 2^31
+    blocks_per_row = (ctx + block - 1) // block
+    pool = torch.zeros(2, kv_heads, 4 * block, d, dtype=torch.bfloat16, device="cuda")
+    tables = torch.zeros(rows, blocks_per_row, dtype=torch.int32, device="cuda")
+    query = torch.ones(rows, heads * d, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(rows, heads * d, dtype=torch.bfloat16, device="cuda")
+    lens = torch.full((rows,), 100, dtype=torch.int32, device="cuda")
+    params = runner.decode_params(query, pool, tables, lens, heads, kv_heads, d, block, 0.088, out, max_context=100)
+    ws = runner.paged_decode(params)  # a valid call: every span record written
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    lens.fill_(ctx)  # max_context stays 100: the contract is broken
+    import ctypes
+    from gaudirt_amd import capi
+    lib = capi.load()
+    assert lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0  # routed to the balanced schedule
+    need = lib.gk_paged_decode_workspace_bytes(ctypes.byref(params))
+    capi.check(lib.gk_paged_decode(ctypes.byref(params), ctypes.c_void_p(ws.data_ptr()), need,
+                                   capi.current_stream()))
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()

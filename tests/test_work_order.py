@@ -1,4 +1,5 @@
-"""CPU test of the prefill kernel's work order inside one XCD's share (no GPU).
+"""CPU test of the prefill kernel's work order inside one XCD's share and of the
+balanced decode schedule's 32-bit tile gate (no GPU).
 
 Builds tests/work_order_test.cpp against gaudirt_amd/csrc/work_order.hpp (the
 code the kernel runs) with g++ and runs it: every share of many launch shapes

@@ -3,6 +3,7 @@
 // share of many launch shapes it checks what the order must be: a
 // permutation of the share, row tiles non-increasing, ascending items within
 // one row tile. Prints OK on success.
+#include <algorithm>
 #include <cstdio>
 #include <vector>
 
@@ -84,10 +85,69 @@ void check_fast_div() {
   }
 }
 
+// The balanced decode schedule's tile count per row against a brute-force
+// count of the tiles holding visible keys, and the host gate
+// (stream_tiles_fit) against the kernel's own overflow test: whenever the
+// gate passes, a batch of rows at max_context, under any window, numbers its
+// tiles with total + wgs below 2^31.
+void check_stream_gate() {
+  for (int ts : {16, 32}) {
+    for (int window : {0, 1, 2, 15, 16, 17, 31, 32, 33, 100, 513, 4096}) {
+      for (int ctx = 0; ctx <= 1200; ++ctx) {
+        const int left = gk::visible_left(ctx, window);
+        int brute = 0;
+        for (int tile = 0; tile * ts < ctx; ++tile)
+          if ((tile + 1) * ts > left) ++brute;
+        if (brute == 0) brute = 1;  // an empty row owns one masked tile
+        const int count = gk::stream_row_tile_count(ctx, window, ts);
+        if (count != brute || count > ctx / ts + 2) {
+          if (failures++ < 10)
+            std::printf("ts=%d window=%d ctx=%d: count %d, brute force %d\n", ts, window, ctx, count, brute);
+          return;
+        }
+      }
+    }
+  }
+  const int64_t limit = int64_t(1) << 31;
+  for (int ts : {16, 32}) {
+    for (int64_t wgs : {int64_t(1), int64_t(256), int64_t(1024), int64_t(4096)}) {
+      for (int64_t units : {int64_t(1), int64_t(7), int64_t(1023), int64_t(65535), int64_t(65535) * 8 * 4}) {
+        // The largest per-row tile bound n = max_context / ts + 2 the gate admits.
+        const int64_t n_max = (limit - 1 - wgs) / units;
+        if (n_max < 2) continue;
+        const int64_t mc_fit = (n_max - 2) * ts + ts - 1, mc_over = (n_max - 1) * ts;
+        if (!gk::stream_tiles_fit(units, mc_fit, ts, wgs) || gk::stream_tiles_fit(units, mc_over, ts, wgs)) {
+          if (failures++ < 10)
+            std::printf("ts=%d wgs=%lld units=%lld: gate boundary not at max_context %lld / %lld\n", ts,
+                        (long long)wgs, (long long)units, (long long)mc_fit, (long long)mc_over);
+          return;
+        }
+        if (mc_fit > 0x7fffffff) continue;  // row_context is int32
+        // Every row at mc_fit under the windows that maximise its tiles.
+        for (int window : {0, ts - 1, ts + 1, 2 * ts - 1, (int)std::min<int64_t>(mc_fit, 0x7fffffff)}) {
+          const int64_t total = units * gk::stream_row_tile_count((int)mc_fit, window, ts);
+          if (total + wgs >= limit) {
+            if (failures++ < 10)
+              std::printf("ts=%d wgs=%lld units=%lld window=%d: gate passed but total %lld + wgs reaches 2^31\n", ts,
+                          (long long)wgs, (long long)units, window, (long long)total);
+            return;
+          }
+        }
+      }
+    }
+  }
+  // Degenerate inputs never pass.
+  if (gk::stream_tiles_fit(-1, 100, 32, 1024) || gk::stream_tiles_fit(1, -1, 32, 1024) ||
+      gk::stream_tiles_fit(1, 100, 32, 0)) {
+    if (failures++ < 10) std::printf("stream_tiles_fit accepted a negative or empty size\n");
+  }
+}
+
 }  // namespace
 
 int main() {
   check_fast_div();
+  check_stream_gate();
   // C4: 8 sequences x 8 kv heads x 8 row tiles.
   check_launch(512, 8);
   // Every small shape, every alignment of a share against the row tiles.
