@@ -64,8 +64,8 @@ class BlockAllocator {
   // Waits for the pending producers of free blocks, then returns fully free slabs.
   int empty_cache();
   AllocatorStats stats();
-  // Message of the last failed call.
-  const std::string& error() const { return error_; }
+  // Message of the calling thread's last failed call (kept per thread).
+  static const std::string& error();
 
  private:
   struct Block {
@@ -90,7 +90,6 @@ class BlockAllocator {
   std::set<std::pair<uint64_t, uintptr_t>> free_;    // free blocks by (size, address)
   std::vector<std::pair<uintptr_t, uint64_t>> slabs_;  // base, bytes (0, 0 once returned)
   std::vector<EventHandle> spare_events_;
-  std::string error_;
   std::mutex mutex_;
 };
 

@@ -32,10 +32,19 @@ BlockAllocator::~BlockAllocator() {
   for (auto event : spare_events_) runtime_.event_destroy(event, ignored);
 }
 
+namespace {
+// Message of the calling thread's last failed call: a failing call records it
+// in the thread that made the call, so a concurrent failure on another thread
+// cannot rewrite it while the caller reads it.
+thread_local std::string t_last_error;
+}  // namespace
+
 int BlockAllocator::fail(int code, std::string message) {
-  error_ = std::move(message);
+  t_last_error = std::move(message);
   return code;
 }
+
+const std::string& BlockAllocator::error() { return t_last_error; }
 
 int BlockAllocator::add_slab(uint64_t size) {
   uint64_t bytes = std::max(size, slab_bytes_);
