@@ -11,9 +11,15 @@ from the 256 MB last-level cache that the previous step filled.
 Prints ONE JSON line: value = decode tokens/s (sequences per second of one
 layer's attention step), the HBM roofline of the decode kernel measured with
 HIP events on the launch stream, and the CPU baseline (the C oracle, a
-restatement of the reference's direct_bf16_pv, on the host's cores).
+restatement of the reference's direct_bf16_pv, on the host's cores). With the
+default headline workload (c2) the same line carries `secondary`: the other
+GPU configurations (c3 fused store + decode, c5 long-context decode: HBM
+roofline; c4 prefix-shared prefill: MFMA roofline), each timed the same way in
+the same process after the headline, `--steps` steps each (c4 after 1000
+warm-up steps).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20 (c4: 1000)] [--workload c2] [--no-cpu]
+                    [--no-secondary]
 """
 
 import argparse
@@ -40,7 +46,10 @@ WORKLOADS = {
           "ctx log-U[1024,32768], 8192-block pool, split-K",
     "c4": "prefix-shared chunked prefill: 8 sequences x 512-row causal chunks on a shared 2048-token prefix, "
           "32 q / 8 kv heads, head_dim 128, block 128",
+    "c2g2": "c2 at GQA group 2: batch 64, 16 q / 8 kv heads, head_dim 128, block 128, ctx U[512,4096], "
+            "4096-block bf16 pool",
 }
+C4_WARMUP = 1000
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -56,12 +65,15 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = library choice)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="headline workload only (no c3/c4/c5 entries after a c2 headline)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
     return ap.parse_args()
 
 
-# The dominant kernel of each workload, as rocprofv3 names it (template
-# arguments: head_dim, softcap, slot-lookup mode).
+# The dominant kernel of each workload with the library's own partition
+# choice, as rocprofv3 names it (template arguments: head_dim, softcap,
+# slot-lookup mode).
 DOMINANT_KERNEL = {
     "c2": "decode_stream_kernel<128, false, 0>",
     "c3": "decode_stream_kernel<128, false, 0>",
@@ -70,12 +82,17 @@ DOMINANT_KERNEL = {
 }
 
 
-def measured_traffic(workload, root=ROOT):
+def measured_traffic(workload, partition=0, root=ROOT):
     """HBM bytes per launch of the workload's dominant kernel, as last measured with
     rocprofv3 PMC (FETCH_SIZE x2 + WRITE_SIZE) and recorded with its command in
-    profiles/<kernel>_<workload>_traffic.md. None when no measurement exists, or when
+    profiles/<kernel>_<workload>_traffic.md. None when no measurement exists, when
     the file measured another kernel than the one this build launches (its
-    `kernel:` line must name DOMINANT_KERNEL[workload])."""
+    `kernel:` line must name DOMINANT_KERNEL[workload]), or when the decode step
+    did not run the balanced schedule (`partition`, the library's
+    gk_paged_decode_partition_tokens for the benchmarked parameters, non-zero:
+    the partitioned kernel ran instead of DOMINANT_KERNEL)."""
+    if partition != 0 or workload not in DOMINANT_KERNEL:
+        return None
     kernel = DOMINANT_KERNEL[workload]
     path = os.path.join(root, "profiles", f"{kernel.split('<')[0]}_{workload}_traffic.md")
     recorded, traffic = None, None
@@ -150,14 +167,14 @@ def host_cpu():
             + (f", OMP_NUM_THREADS={omp}" if omp else "") + ")")
 
 
-def prefill_bench(args):
-    """Workload C4: one gk_paged_prefill call per step; MFMA roofline (causal-exact FLOPs)."""
+def prefill_run(lib, steps, warmup, seed):
+    """Workload C4: one gk_paged_prefill call per step, timed with HIP events on the
+    launch stream. Returns (ms per step, TFLOP/s, the case)."""
     import torch
 
     from gaudirt_amd import capi, workloads
 
-    lib = capi.load()
-    pc = workloads.DevicePrefillCase(seed=args.seed)
+    pc = workloads.DevicePrefillCase(seed=seed)
     stream = torch.cuda.current_stream()
     p = capi.PrefillParams()
     p.query, p.q_row_stride = pc.query.data_ptr(), pc.query.stride(0)
@@ -170,52 +187,49 @@ def prefill_bench(args):
     p.scale, p.softcap, p.sliding_window = pc.scale, 0.0, -1
     p.out, p.out_row_stride = pc.out.data_ptr(), pc.out.stride(0)
     hstream = ctypes.c_void_p(stream.cuda_stream)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         capi.check(lib.gk_paged_prefill(ctypes.byref(p), hstream))
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         capi.check(lib.gk_paged_prefill(ctypes.byref(p), hstream))
     end.record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms = start.elapsed_time(end) / steps
     tflops = pc.flops() / (ms * 1e-3) / 1e12
     print(f"[bench] c4: {ms * 1e3:.1f} us/step, {tflops:.1f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of "
           f"{MFMA_BF16_PEAK_TFLOPS:.0f}), {pc.rows / (ms * 1e-3):.4g} query rows/s", file=sys.stderr, flush=True)
+    return ms, tflops, pc
+
+
+def prefill_roofline(tflops):
+    return {"bound": "mfma", "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": measured_traffic("c4")}
+
+
+def prefill_bench(args):
+    """C4 as the headline workload: its own JSON line (MFMA roofline, causal-exact FLOPs)."""
+    from gaudirt_amd import capi
+
+    ms, tflops, pc = prefill_run(capi.load(), args.steps, args.warmup, args.seed)
     print(json.dumps({
         "metric": "prefix-shared chunked prefill attention TFLOP/s (causal-exact), 1 MI355X",
         "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic", "config": {"workload": f"c4: {WORKLOADS['c4']}", "flops_per_step": pc.flops()},
-        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": measured_traffic("c4")},
-        "cpu_baseline": None}), flush=True)
+        "roofline": prefill_roofline(tflops), "cpu_baseline": None}), flush=True)
 
 
-def main():
-    args = parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the decode path does not shard across GPUs here", file=sys.stderr)
-        sys.exit(2)
-    if args.warmup is None:
-        args.warmup = 1000 if args.workload == "c4" else 20
-    if args.workload == "c4":
-        import torch
-        assert torch.cuda.is_available(), "bench.py needs an MI355X"
-        torch.cuda.set_device(0)
-        return prefill_bench(args)
-
-    import numpy as np
+def decode_run(lib, workload, steps, warmup, table_sets, seed, partition):
+    """One gk_paged_decode call per step over the whole batch of a decode workload,
+    timed with HIP events on the launch stream; consecutive steps rotate over
+    `table_sets` disjoint block-table sets. Returns a dict of the timing and the case."""
     import torch
 
     from gaudirt_amd import capi, workloads
 
-    assert torch.cuda.is_available(), "bench.py needs an MI355X"
-    torch.cuda.set_device(0)
-    lib = capi.load()
-    dc = workloads.DeviceDecodeCase(args.workload, seed=args.seed, table_sets=args.table_sets)
+    dc = workloads.DeviceDecodeCase(workload, seed=seed, table_sets=table_sets)
     stream = torch.cuda.current_stream()
     hstream = ctypes.c_void_p(stream.cuda_stream)
 
@@ -228,7 +242,7 @@ def main():
         p.row_request, p.row_context, p.rows = None, dc.d_lens.data_ptr(), dc.batch
         p.q_heads, p.kv_heads, p.head_dim = dc.heads, dc.kv_heads, dc.head_dim
         p.scale, p.softcap, p.sliding_window = dc.scale, 0.0, -1
-        p.max_context, p.partition_tokens = int(dc.lens.max()), args.partition
+        p.max_context, p.partition_tokens = int(dc.lens.max()), partition
         p.out, p.out_row_stride = dc.out.data_ptr(), dc.out.stride(0)
         if dc.store:
             p.new_key, p.new_value = dc.new_key.data_ptr(), dc.new_value.data_ptr()
@@ -237,13 +251,13 @@ def main():
         params.append(p)
     need = max(lib.gk_paged_decode_workspace_bytes(ctypes.byref(p)) for p in params)
     workspace = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
-    partition = lib.gk_paged_decode_partition_tokens(ctypes.byref(params[0]))
+    chosen = lib.gk_paged_decode_partition_tokens(ctypes.byref(params[0]))
 
     def step(i):
         capi.check(lib.gk_paged_decode(ctypes.byref(params[i % len(params)]),
                                        ctypes.c_void_p(workspace.data_ptr()), need, hstream))
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
 
@@ -251,21 +265,90 @@ def main():
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     start.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    ms_per_step = start.elapsed_time(end) / args.steps
+    ms_per_step = start.elapsed_time(end) / steps
+    del workspace
 
     step_bytes = dc.step_bytes()
     kv_bytes = dc.kv_bytes()
     seconds = ms_per_step * 1e-3
     achieved = step_bytes / seconds / 1e9
     tokens_per_s = dc.batch / seconds
-    print(f"[bench] {args.workload}: {ms_per_step * 1e3:.1f} us/step, {tokens_per_s:.4g} tokens/s, "
+    print(f"[bench] {workload}: {ms_per_step * 1e3:.1f} us/step, {tokens_per_s:.4g} tokens/s, "
           f"{achieved:.1f} GB/s ({achieved / HBM_PEAK_GBPS:.1%} of peak), KV {kv_bytes / 1e9:.4f} GB/step, "
-          f"partition {partition}, wall {wall:.2f} s", file=sys.stderr, flush=True)
+          f"partition {chosen}, wall {wall:.2f} s", file=sys.stderr, flush=True)
+    return {
+        "case": dc,
+        "ms_per_step": ms_per_step,
+        "tokens_per_s": tokens_per_s,
+        "partition": int(chosen),
+        "table_sets": len(params),
+        "kv_read_gbps": kv_bytes / seconds / 1e9,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": measured_traffic(workload, int(chosen)),
+        },
+    }
+
+
+def secondary_runs(lib, args):
+    """C3, C5 (HBM roofline) and C4 (MFMA roofline) after the headline, in the same
+    process, `args.steps` timed steps each."""
+    import torch
+
+    out = {}
+    for workload in ("c3", "c5"):
+        r = decode_run(lib, workload, args.steps, args.warmup, args.table_sets, args.seed, 0)
+        dc = r.pop("case")
+        out[workload] = {
+            "workload": f"{workload}: {WORKLOADS[workload]}",
+            "value": r["tokens_per_s"], "unit": "tokens/s", "ms_per_step": r["ms_per_step"],
+            "steps": args.steps, "warmup": args.warmup, "split_k_partition": r["partition"],
+            "mean_context": float(dc.lens.mean()), "max_context": int(dc.lens.max()),
+            "roofline": r["roofline"],
+        }
+        del dc
+        torch.cuda.empty_cache()
+    ms, tflops, pc = prefill_run(lib, args.steps, C4_WARMUP, args.seed)
+    out["c4"] = {
+        "workload": f"c4: {WORKLOADS['c4']}",
+        "value": tflops, "unit": "TFLOP/s", "ms_per_step": ms, "steps": args.steps, "warmup": C4_WARMUP,
+        "flops_per_step": pc.flops(), "roofline": prefill_roofline(tflops),
+    }
+    del pc
+    torch.cuda.empty_cache()
+    return out
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the decode path does not shard across GPUs here", file=sys.stderr)
+        sys.exit(2)
+    if args.warmup is None:
+        args.warmup = C4_WARMUP if args.workload == "c4" else 20
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    torch.cuda.set_device(0)
+    if args.workload == "c4":
+        return prefill_bench(args)
+
+    from gaudirt_amd import capi
+
+    lib = capi.load()
+    r = decode_run(lib, args.workload, args.steps, args.warmup, args.table_sets, args.seed, args.partition)
+    dc = r["case"]
 
     cpu = None
     if not args.no_cpu:
@@ -274,12 +357,12 @@ def main():
 
     line = {
         "metric": METRIC,
-        "value": tokens_per_s,
+        "value": r["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -294,21 +377,18 @@ def main():
             "block_size": dc.block_size,
             "mean_context": float(dc.lens.mean()),
             "max_context": int(dc.lens.max()),
-            "split_k_partition": int(partition),
-            "table_sets": len(params),
+            "split_k_partition": r["partition"],
+            "table_sets": r["table_sets"],
             "seed": args.seed,
-            "kv_read_gbps": kv_bytes / seconds / 1e9,
+            "kv_read_gbps": r["kv_read_gbps"],
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": measured_traffic(args.workload),
-        },
+        "roofline": r["roofline"],
         "cpu_baseline": cpu,
     }
+    if args.workload == "c2" and not args.no_secondary:
+        del dc, r
+        torch.cuda.empty_cache()
+        line["secondary"] = secondary_runs(lib, args)
     print(json.dumps(line), flush=True)
 
 

@@ -24,6 +24,10 @@ def test_traffic_records_name_the_shipping_kernel(tmp_path):
     good.write_text("kernel: decode_stream_kernel<128, false, false>\ntraffic_bytes_per_launch: 123\n")
     assert bench.measured_traffic("c2", root=str(tmp_path)) is None  # an older template: stale
     assert bench.measured_traffic("c5", root=str(tmp_path)) is None  # no record: null, not a guess
+    # A step the library routed to the partitioned kernel did not run the recorded kernel.
+    good.write_text(f"kernel: {bench.DOMINANT_KERNEL['c2']}\ntraffic_bytes_per_launch: 123\n")
+    assert bench.measured_traffic("c2", partition=2048, root=str(tmp_path)) is None
+    assert bench.measured_traffic("c2g2", root=str(tmp_path)) is None
     for workload in ("c2", "c3", "c4", "c5"):
         value = bench.measured_traffic(workload)
         kernel = bench.DOMINANT_KERNEL[workload]
