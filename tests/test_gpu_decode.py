@@ -4,6 +4,9 @@ Tolerance (the benchmark's parity gate): bf16 outputs within max-abs 2e-2 and me
 2e-3 of the reference implementation (direct_bf16_pv, and tiled_bf16_pv with
 the reference's 512-key tile), plus the reference's own relative-L2 gates
 (<= 1e-2 vs fp64, <= 5e-3 vs tiled; tests/paged_attention_reference.py:60-69).
+On the benchmark configurations (C1, C2, C3, C5) the 2e-2 bound is flat; the
+synthetic geometries allow one bf16 ulp where it exceeds 2e-2 (|out| >= 4),
+where even the exact answer rounded to bf16 can differ from direct_bf16_pv.
 """
 
 import math
@@ -19,7 +22,8 @@ pytestmark = pytest.mark.gpu
 MAX_ABS, MEAN_ABS = 2e-2, 2e-3
 
 
-def check_against_oracle(case, actual_bits, threads=16):
+def check_against_oracle(case, actual_bits, threads=16, flat=False):
+    """flat: the benchmark gate taken literally (no ulp allowance), for C1-C5."""
     p = case.oracle_problem()
     direct = orc.direct_bf16_pv(p, threads)
     tiled = orc.tiled_bf16_pv(p, 512, threads)
@@ -27,6 +31,8 @@ def check_against_oracle(case, actual_bits, threads=16):
     assert np.isfinite(orc.bf16_to_f32(actual_bits)).all()
     for name, ref in (("direct_bf16_pv", direct), ("tiled_bf16_pv", tiled)):
         max_abs, mean_abs = orc.check_tolerance(actual_bits, ref, MAX_ABS, MEAN_ABS)
+        if flat:
+            orc.check_flat_gate(actual_bits, ref, MAX_ABS, MEAN_ABS)
         ulp_only = orc.ulp_allowance_count(actual_bits, ref, MAX_ABS)
         print(f"{name}: max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} "
               f"ulp_allowance_only={ulp_only} of {actual_bits.size}", flush=True)
@@ -45,13 +51,13 @@ def runner():
 def test_c1_decode(runner):
     case = cases.c1_case()
     print("c1 lens", case.lens.tolist(), flush=True)
-    check_against_oracle(case, runner.run_case(case))
+    check_against_oracle(case, runner.run_case(case), flat=True)
 
 
 @pytest.mark.parametrize("partition", [32, 64, 128, 512])
 def test_c1_decode_split_k_partitions(runner, partition):
     case = cases.c1_case(seed=77)
-    check_against_oracle(case, runner.run_case(case, partition=partition))
+    check_against_oracle(case, runner.run_case(case, partition=partition), flat=True)
 
 
 @pytest.mark.parametrize("geometry", [(8, 8, 64), (14, 2, 64), (56, 8, 128), (9, 3, 64), (16, 8, 256), (64, 8, 128),
@@ -107,7 +113,7 @@ def test_full_size_decode(runner, name):
     torch.cuda.synchronize()
     del ws
     actual = runner.bits_of(dc.out)
-    check_against_oracle(cases.host_case(dc), actual)
+    check_against_oracle(cases.host_case(dc), actual, flat=True)
 
 
 def test_c3_fused_store_then_decode(runner):
@@ -134,4 +140,4 @@ def test_c3_fused_store_then_decode(runner):
             assert torch.equal(dc.pool[kind, h][~touched].view(torch.int16),
                                before[kind, h][~touched].view(torch.int16)), (kind, h)
     del before
-    check_against_oracle(cases.host_case(dc), runner.bits_of(dc.out))
+    check_against_oracle(cases.host_case(dc), runner.bits_of(dc.out), flat=True)

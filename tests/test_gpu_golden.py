@@ -3,8 +3,8 @@
 The C1 decode case and the d 64 prefill case of tests/golden/reference_vectors.npz
 run through the C ABI (gk_paged_decode, gk_paged_prefill) and are compared with
 the reference's direct_bf16_pv and tiled_bf16_pv outputs
-(tests/paged_attention_reference.py:6-59) under the parity gate: bf16 outputs
-within max-abs 2e-2 (one bf16 ulp where that is larger) and mean-abs 2e-3.
+(tests/paged_attention_reference.py:6-59) under the parity gate taken
+literally: bf16 outputs within a flat max-abs 2e-2 and mean-abs 2e-3.
 """
 
 import numpy as np
@@ -35,9 +35,8 @@ def runner():
 
 def gate(name, actual, ref):
     assert np.isfinite(orc.bf16_to_f32(actual)).all()
-    max_abs, mean_abs = orc.check_tolerance(actual, ref, MAX_ABS, MEAN_ABS)
-    print(f"{name}: max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} "
-          f"ulp_allowance_only={orc.ulp_allowance_count(actual, ref, MAX_ABS)}", flush=True)
+    max_abs, mean_abs = orc.check_flat_gate(actual, ref, MAX_ABS, MEAN_ABS)
+    print(f"{name}: max_abs={max_abs:.3e} mean_abs={mean_abs:.3e}", flush=True)
 
 
 @pytest.mark.parametrize("partition", [0, 64])

@@ -8,9 +8,9 @@ the token-granular map); the 28672 + 4096 = 32768-key chunk of the same file
 (:1586-1598, 56 q / 8 kv heads, head_dim 128) runs through the C ABI with
 128-token blocks; workload C4 is checked on every row. Each case checks every
 listed row against direct_bf16_pv (max-abs 2e-2, mean-abs 2e-3), the
-relative-L2 gates against fp64 (1e-2) and tiled_bf16_pv (5e-3), and prints the
-worst errors and how many elements passed only through the one-ulp allowance
-of the output gate.
+relative-L2 gates against fp64 (1e-2) and tiled_bf16_pv (5e-3). The 2e-2
+bound is flat (the benchmark gate taken literally, no one-ulp allowance) on
+every case here.
 """
 
 import math
@@ -41,8 +41,9 @@ def report(name, actual, problem):
     """Every gate of the prefill parity on these rows; prints the figures."""
     direct = orc.direct_bf16_pv(problem)
     assert np.isfinite(orc.bf16_to_f32(actual)).all()
-    max_abs, mean_abs = orc.check_tolerance(actual, direct, MAX_ABS, MEAN_ABS)
+    max_abs, mean_abs = orc.check_flat_gate(actual, direct, MAX_ABS, MEAN_ABS)
     ulp_only = orc.ulp_allowance_count(actual, direct, MAX_ABS)
+    assert ulp_only == 0
     tiled = orc.tiled_bf16_pv(problem, 512)
     e64, etiled = orc.isolated_errors(orc.bf16_to_f32(actual), orc.fp64_bf16(problem), orc.bf16_to_f32(tiled))
     print(f"{name}: rows={actual.shape[0]} max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} "

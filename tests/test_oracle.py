@@ -361,6 +361,31 @@ def test_bf16_ulp_and_tolerance_gate():
         orc.check_tolerance(off_small, ref, 2e-2, 2e-2)
 
 
+def test_flat_gate_known_answers():
+    # The literal benchmark gate: 2e-2 flat, no ulp allowance.
+    ref = orc.bf16_from_f32(np.float32([0.5, 1.0, -2.0, 0.0]))
+    # 163 / 8192 and 164 / 8192: the bf16 numbers on either side of 0.02.
+    at_bound = orc.bf16_from_f32(np.float32([0.5, 1.0, -2.0, 163 / 8192]))
+    orc.check_flat_gate(at_bound, ref, 2e-2, 2e-2)
+    over = orc.bf16_from_f32(np.float32([0.5, 1.0, -2.0, 164 / 8192]))
+    with pytest.raises(AssertionError):
+        orc.check_flat_gate(over, ref, 2e-2, 2e-2)
+    # One ulp at |x| >= 4 passes check_tolerance but not the flat gate.
+    big = orc.bf16_from_f32(np.float32([4.0]))
+    big_up = orc.bf16_from_f32(np.float32([4.03125]))
+    orc.check_tolerance(big_up, big, 2e-2, 5e-2)
+    with pytest.raises(AssertionError):
+        orc.check_flat_gate(big_up, big, 2e-2, 5e-2)
+    with pytest.raises(AssertionError):
+        orc.check_flat_gate(orc.bf16_from_f32(np.float32([np.nan])), big, 2e-2, 2e-2)
+    # The mean bound: 0.015 on every element is within max_abs but not a 2e-3 mean.
+    base = orc.bf16_from_f32(np.float32([0.25] * 8))
+    shifted = orc.bf16_from_f32(np.float32([0.265625] * 8))
+    with pytest.raises(AssertionError):
+        orc.check_flat_gate(shifted, base, 2e-2, 2e-3)
+    assert orc.check_flat_gate(shifted, base, 2e-2, 2e-2) == (0.015625, 0.015625)
+
+
 def test_exact_answer_is_one_ulp_from_direct_bf16_pv_at_large_outputs():
     """Why the output gate allows one bf16 ulp where it exceeds 2e-2: on the
     nanbeige-geometry case of the device tests (56 q / 8 kv heads, d 128,
