@@ -116,9 +116,12 @@ int gk_paged_decode(const gk_decode_params* params, void* workspace, size_t work
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). Same parameters,
  * kernels and results as gk_paged_decode, whose workspace here is a static
- * device array of GK_DECODE_SCRATCH_BYTES that every GPU the library runs on
- * holds until the process ends (located on the first call on each device;
- * the current device must be the stream's). Parameters whose workspace
+ * device array of GK_DECODE_SCRATCH_BYTES that every GPU the library's code
+ * object is loaded on holds until the process ends, whether or not this entry
+ * point is ever called (the torch op path included). The first call on each
+ * device looks up the array's address and the grid size; make it before any
+ * graph capture, after which calls can be captured and replayed (the current
+ * device must be the stream's). Parameters whose workspace
  * (gk_paged_decode_workspace_bytes) exceeds it are rejected with
  * GK_ERR_WORKSPACE before anything is enqueued. All calls on one GPU share the
  * array: calls that overlap on one GPU (on different streams, or from

@@ -126,3 +126,46 @@ def test_scratch_decode_rejects_oversized_workspace(env):
     assert b"static scratch" in lib.gk_last_error()
     torch.cuda.synchronize()
     assert bool(torch.isnan(out).all()), "a rejected call wrote output"
+
+
+def test_scratch_decode_under_graph_capture(env):
+    # The caller this entry point is for: a HIP graph. After one eager call on
+    # the device (which looks up the array's address and the grid size), the
+    # call is captured into a graph with nothing allocated during capture, and
+    # every replay must equal gk_paged_decode on the inputs present at replay
+    # time (the query is rewritten in place between replays, with eager work
+    # and synchronisations in between).
+    torch, capi, lib, runner = env
+    from gaudirt_amd import workloads
+
+    dc = workloads.DeviceDecodeCase("c2")
+    out = torch.full_like(dc.out, float("nan"))
+    params = runner.decode_params(dc.query, dc.pool, dc.d_tables, dc.d_lens, dc.heads, dc.kv_heads, dc.head_dim,
+                                  dc.block_size, dc.scale, out)
+    assert lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0  # balanced schedule + merge
+    capi.check(lib.gk_paged_decode_scratch(ctypes.byref(params), capi.current_stream()))  # first call: set-up
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        capi.check(lib.gk_paged_decode_scratch(ctypes.byref(params), capi.current_stream()))
+    torch.cuda.synchronize()
+
+    want_out = torch.empty_like(dc.out)
+    want_params = runner.decode_params(dc.query, dc.pool, dc.d_tables, dc.d_lens, dc.heads, dc.kv_heads,
+                                       dc.head_dim, dc.block_size, dc.scale, want_out)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    for replay in range(3):
+        dc.query.copy_(torch.randn(dc.query.shape, generator=gen, device="cuda").to(torch.bfloat16))
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ws = runner.paged_decode(want_params)
+        torch.cuda.synchronize()
+        del ws
+        got, want = runner.bits_of(out), runner.bits_of(want_out)
+        print(f"replay {replay}: equal={np.array_equal(got, want)}", flush=True)
+        assert np.array_equal(got, want), replay
+    del graph
