@@ -19,7 +19,15 @@ the same process after the headline, `--steps` steps each (c4 after 1000
 warm-up steps).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20 (c4: 1000)] [--workload c2] [--no-cpu]
-                    [--no-secondary]
+                    [--no-secondary] [--host-overhead]
+
+--host-overhead instead times the drop-in op torch.ops.gaudirt.paged_attn on
+C2's decode step (store of each row's new K/V, then attention), host side and
+GPU side: per step, the host microseconds of building the metadata and
+launching the op, for the reference's host constructor path
+(PagedMetadata(locations, requests, positions, mapping, slots)) and for the
+serving path (PagedMetadata._from_scheduler on device-resident inputs), next
+to the GPU time of the same step. It prints its own JSON line.
 """
 
 import argparse
@@ -67,6 +75,8 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true",
                     help="headline workload only (no c3/c4/c5 entries after a c2 headline)")
+    ap.add_argument("--host-overhead", action="store_true",
+                    help="time the torch op's host side on C2 (metadata + launch) next to its GPU step")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
     return ap.parse_args()
 
@@ -328,6 +338,89 @@ def secondary_runs(lib, args):
     return out
 
 
+def host_overhead(args):
+    """Host and GPU time per decode step of torch.ops.gaudirt.paged_attn on C2."""
+    import numpy as np
+    import torch
+
+    import gaudirt_amd
+    from gaudirt_amd import workloads
+
+    gaudirt_amd.load_extension()
+    dc = workloads.DeviceDecodeCase("c2", seed=args.seed)
+    rows, context, block = dc.batch, int(dc.lens.max()), dc.block_size
+    # The token-granular request map of C2's block tables (-1 past each row's length).
+    t = np.arange(context)
+    mapping = np.where(t[None, :] < dc.lens[:, None],
+                       dc.tables[:, np.minimum(t // block, dc.tables.shape[1] - 1)] * block + t % block, -1)
+    mapping = np.ascontiguousarray(mapping.astype(np.int32))
+    positions = dc.lens.astype(np.int64) - 1
+    locations = mapping[np.arange(rows), positions].astype(np.int64)
+    cpu = {"locations": torch.from_numpy(locations), "requests": torch.arange(rows, dtype=torch.int64),
+           "positions": torch.from_numpy(positions), "mapping": torch.from_numpy(mapping)}
+    dev = {k: v.cuda() for k, v in cpu.items()}
+    prefixes, lengths = positions.tolist(), [1] * rows
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed)
+    k = torch.randn((rows, dc.kv_heads * dc.head_dim), generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn((rows, dc.kv_heads * dc.head_dim), generator=gen, device="cuda").to(torch.bfloat16)
+    key_pool, value_pool = dc.pool[0].transpose(0, 1), dc.pool[1].transpose(0, 1)
+    op = torch.ops.gaudirt.paged_attn.default
+    cls = torch.classes.gaudirt.PagedMetadata
+
+    def host_ctor():
+        m = cls(cpu["locations"], cpu["requests"], cpu["positions"], cpu["mapping"], dc.slots)
+        return op(dc.query, k, v, key_pool, value_pool, m, dc.head_dim, dc.scale)
+
+    def scheduler():
+        m = cls._from_scheduler(dev["locations"], dev["requests"], dev["positions"], dev["mapping"], prefixes,
+                                lengths, dc.slots, None, 0)
+        return op(dc.query, k, v, key_pool, value_pool, m, dc.head_dim, dc.scale)
+
+    def reused(meta):
+        return lambda: op(dc.query, k, v, key_pool, value_pool, meta, dc.head_dim, dc.scale)
+
+    stream = torch.cuda.current_stream()
+    result = {}
+    prebuilt = cls(cpu["locations"], cpu["requests"], cpu["positions"], cpu["mapping"], dc.slots)
+    for name, fn in (("host_constructor", host_ctor), ("from_scheduler", scheduler),
+                     ("metadata_reused", reused(prebuilt))):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        host = []
+        start.record(stream)
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            fn()
+            host.append(time.perf_counter() - t0)
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall_ms = start.elapsed_time(end) / args.steps
+        result[name] = {"host_us_median": statistics.median(host) * 1e6,
+                        "host_us_mean": statistics.fmean(host) * 1e6,
+                        "stream_us_per_step": wall_ms * 1e3}
+        print(f"[bench] host overhead {name}: host {result[name]['host_us_median']:.1f} us/step (median), "
+              f"stream {wall_ms * 1e3:.1f} us/step", file=sys.stderr, flush=True)
+    # The GPU time of one step alone: each step timed between its own events after a sync.
+    gpu = []
+    for _ in range(20):
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        reused(prebuilt)()
+        end.record(stream)
+        torch.cuda.synchronize()
+        gpu.append(start.elapsed_time(end) * 1e3)
+    result["gpu_step_us_median"] = statistics.median(gpu)
+    print(f"[bench] host overhead: GPU step alone {result['gpu_step_us_median']:.1f} us", file=sys.stderr,
+          flush=True)
+    print(json.dumps({"metric": "paged_attn host overhead per decode step (c2), 1 MI355X", "unit": "us",
+                      "steps": args.steps, "warmup": args.warmup, "rows": rows, "context": context,
+                      "token_granular_map": True, **result}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -341,6 +434,8 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     torch.cuda.set_device(0)
+    if args.host_overhead:
+        return host_overhead(args)
     if args.workload == "c4":
         return prefill_bench(args)
 

@@ -14,18 +14,31 @@ for it (python/gaudirt/__init__.py, src/bridge/generic_private_use1.cpp:430-540)
   stream-ordered block allocator, and ``kv_pool_views(pool, layer)`` its
   ``(key_pool, value_pool)`` views ``[slots, kv_heads, head_dim]``.
 
+- ``set_batch_invariant_decode(enabled, partition_tokens=2048)``: decode rows
+  of ``paged_attn`` on fixed split-K partitions, so each row's output is a
+  function of that row alone, bit for bit (the reference's single-row replay,
+  tests/paged_attention_smoke.py:145-150); off by default, where the balanced
+  schedule's split points depend on the whole batch. The environment variable
+  ``GAUDIRT_AMD_BATCH_INVARIANT_DECODE`` (``1``, or a partition in keys) turns
+  it on when the extension loads.
+
 The extension is loaded on first use of any of these names (or by
 ``load_extension()``); a missing build raises ImportError. There is no other
 implementation behind them.
 """
 
+import os
 import pathlib
 
 _PACKAGE = pathlib.Path(__file__).resolve().parent
 _ext = None
 
 __all__ = ["load_extension", "PagedMetadata", "paged_attn", "allocate_paged_kv", "kv_pool_views",
-           "advance_decode_lengths", "kv_allocator_stats", "paged_attn_kv_tile"]
+           "advance_decode_lengths", "kv_allocator_stats", "paged_attn_kv_tile", "set_batch_invariant_decode",
+           "batch_invariant_decode"]
+
+# Keys per split-K partition of the batch-invariant decode mode.
+BATCH_INVARIANT_PARTITION = 2048
 
 
 def load_extension():
@@ -44,7 +57,22 @@ def load_extension():
     from . import _C as ext
     _register_fakes(torch)
     _ext = ext
+    env = os.environ.get("GAUDIRT_AMD_BATCH_INVARIANT_DECODE", "").strip()
+    if env and env != "0":
+        set_batch_invariant_decode(True, BATCH_INVARIANT_PARTITION if env == "1" else int(env))
     return ext
+
+
+def set_batch_invariant_decode(enabled=True, partition_tokens=BATCH_INVARIANT_PARTITION):
+    """Decode rows of paged_attn on fixed partitions of `partition_tokens` keys (a
+    multiple of 32 up to 8192): every row's output then depends on that row alone.
+    Off: the library's balanced schedule (the default; faster on skewed batches)."""
+    load_extension()._set_decode_partition(int(partition_tokens) if enabled else 0)
+
+
+def batch_invariant_decode():
+    """The fixed decode partition in keys, or 0 when the library chooses."""
+    return load_extension()._decode_partition()
 
 
 def _register_fakes(torch):

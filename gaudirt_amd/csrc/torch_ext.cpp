@@ -23,6 +23,7 @@
 
 #include <algorithm>
 #include <array>
+#include <atomic>
 #include <bit>
 #include <cmath>
 #include <cstring>
@@ -41,6 +42,15 @@ namespace {
 void check_gk(int rc, const char* what) {
   TORCH_CHECK(rc == GK_OK, what, ": ", gk_last_error());
 }
+
+// Split-K partition of the decode rows of paged_attn. 0 (the default) leaves
+// it to the library: the balanced schedule, whose split points depend on the
+// whole batch, so a row's last bits can change with the rows around it. A
+// fixed partition of that many keys (the partitioned kernel) makes every
+// decode row's output a function of that row alone, bit for bit: the
+// reference's single-row replay equals the batched row
+// (tests/paged_attention_smoke.py:145-150).
+std::atomic<int32_t> g_decode_partition{0};
 
 hipStream_t current_stream() { return c10::hip::getCurrentHIPStream().stream(); }
 
@@ -171,6 +181,24 @@ struct PlanInfo {
   hipStream_t stream = nullptr;
   at::Tensor storage;  // the plan's own device buffer
   int64_t block_table_offset = 0;
+  // Read in place instead of from `storage` when defined: the token-granular
+  // request map as the block tables (page 1), and the metadata's own row
+  // requests when every row is a decode row in batch order.
+  // requests, visible keys and the identity row map when every row is a
+  // decode row in batch order (a serving decode step needs no plan upload).
+  at::Tensor block_tables_ref, row_request_ref, row_context_ref;
+  const int32_t* block_tables(const int32_t* words) const {
+    return block_tables_ref.defined() ? block_tables_ref.data_ptr<int32_t>() : words + block_table_offset;
+  }
+  const int32_t* row_request(const int32_t* words) const {
+    return row_request_ref.defined() ? row_request_ref.data_ptr<int32_t>() : words + row_request_offset;
+  }
+  const int32_t* row_context(const int32_t* words) const {
+    return row_context_ref.defined() ? row_context_ref.data_ptr<int32_t>() : words + row_context_offset;
+  }
+  const int32_t* row_map(const int32_t* words) const {
+    return row_context_ref.defined() ? nullptr : words + row_map_offset;
+  }
   // Rows attended one by one (gk_paged_decode): request, visible keys and the
   // batch row of each.
   int64_t decode_rows = 0, decode_max_context = 0;
@@ -234,12 +262,29 @@ class PagedMetadata : public torch::CustomClassHolder {
                 "GaudiRT: paged metadata dimensions outside supported range");
     // Whole-tensor checks first, then one failure code per row; the first
     // failing row reports its first failing check, so the messages and their
-    // order are those of the reference's row-by-row scan.
-    const auto map64 = mapping.to(at::kLong);
-    TORCH_CHECK(map64.ge(-1).all().item<bool>() && map64.lt(slots).all().item<bool>(),
-                "GaudiRT: request-to-token slot is out of range");
-    const auto map32 = map64.to(at::kInt);
-    mapping_h_.assign(map32.data_ptr<int32_t>(), map32.data_ptr<int32_t>() + map32.numel());
+    // order are those of the reference's row-by-row scan. The request map is
+    // range-checked in one pass while it is copied to the host vector.
+    const int64_t map_n = mapping.numel();
+    mapping_h_.resize(map_n);
+    bool map_in_range = true;
+    if (mapping.scalar_type() == at::kInt) {
+      const int32_t* src = mapping.data_ptr<int32_t>();
+      int32_t lo = 0, hi = 0;
+      if (map_n) lo = hi = src[0];
+      for (int64_t i = 0; i < map_n; ++i) {
+        lo = std::min(lo, src[i]);
+        hi = std::max(hi, src[i]);
+      }
+      map_in_range = lo >= -1 && hi < slots;
+      if (map_in_range) std::memcpy(mapping_h_.data(), src, map_n * sizeof(int32_t));
+    } else {
+      const int64_t* src = mapping.data_ptr<int64_t>();
+      for (int64_t i = 0; i < map_n && map_in_range; ++i) {
+        map_in_range = src[i] >= -1 && src[i] < slots;
+        mapping_h_[i] = static_cast<int32_t>(src[i]);
+      }
+    }
+    TORCH_CHECK(map_in_range, "GaudiRT: request-to-token slot is out of range");
     const auto loc = locations.to(at::kLong), req = requests.to(at::kLong), pos = positions.to(at::kLong);
     const int64_t* loc_p = loc.data_ptr<int64_t>();
     const int64_t* req_p = req.data_ptr<int64_t>();
@@ -279,47 +324,66 @@ class PagedMetadata : public torch::CustomClassHolder {
     for (size_t k = 0; k + 1 < run_starts.size(); ++k)
       sequences_.push_back({run_starts[k], run_starts[k + 1] - run_starts[k], positions_h_[run_starts[k]]});
     // Every request's visible prefix (positions up to its last row) must have
-    // slots, none of them the output slot of another (request, position).
+    // slots, none of them the output slot of another (request, position). The
+    // written slots also go into a 2^16-bit filter (slot mod 2^16), so the scan
+    // looks a slot up among them only when its filter bit is set.
     max_position_.assign(request_count, -1);
     for (int64_t i = 0; i < m; ++i)
       max_position_[requests_h_[i]] = std::max(max_position_[requests_h_[i]], positions_h_[i]);
+    std::vector<uint64_t> written(1024, 0);
+    for (int64_t i = 0; i < m; ++i) written[(loc_p[i] >> 6) & 1023] |= uint64_t{1} << (loc_p[i] & 63);
     const auto writer_of = [&](int32_t slot) -> int64_t {  // the row writing `slot`, or -1
       const auto it = std::lower_bound(by_slot.begin(), by_slot.end(), slot,
                                        [&](int64_t row, int32_t s) { return loc_p[row] < s; });
       return it != by_slot.end() && loc_p[*it] == slot ? *it : -1;
     };
+    // The same scan finds the page size of the map: the largest power of two
+    // P <= 1024 such that each visible token t sits at map[t - t % P] + t % P
+    // with map[t - t % P] a multiple of P. That holds exactly when every break
+    // of the map (t = 0, or map[t] != map[t - 1] + 1) has both t and map[t]
+    // divisible by P, so P is the lowest set bit of the OR of those values.
+    uint32_t breaks = 0;
     for (int64_t request = 0; request < request_count; ++request) {
       const int32_t* row_map = mapping_h_.data() + request * context;
       for (int32_t position = 0; position <= max_position_[request]; ++position) {
-        TORCH_CHECK(row_map[position] >= 0, "GaudiRT: missing KV slot in a visible prefix");
-        const int64_t writer = writer_of(row_map[position]);
-        TORCH_CHECK(writer < 0 || (requests_h_[writer] == request && positions_h_[writer] == position),
-                    "GaudiRT: output KV slot aliases another visible prefix position");
+        const int32_t slot = row_map[position];
+        TORCH_CHECK(slot >= 0, "GaudiRT: missing KV slot in a visible prefix");
+        if (position == 0 || slot != row_map[position - 1] + 1)
+          breaks |= static_cast<uint32_t>(position) | static_cast<uint32_t>(slot);
+        if (written[(slot >> 6) & 1023] & (uint64_t{1} << (slot & 63))) {
+          const int64_t writer = writer_of(slot);
+          TORCH_CHECK(writer < 0 || (requests_h_[writer] == request && positions_h_[writer] == position),
+                      "GaudiRT: output KV slot aliases another visible prefix position");
+        }
       }
     }
+    page_ = 1024;
+    while (page_ > 1 && (breaks & static_cast<uint32_t>(page_ - 1))) page_ >>= 1;
     rows_ = m;
     slots_ = slots;
     request_count_ = request_count;
     context_ = context;
-    // One device buffer: header | locations | requests | positions | mapping.
+    // One device buffer: header | locations | requests | positions. The request
+    // map goes to the device only when something reads it there (the
+    // token-granular plan or request_mapping()).
     int64_t cursor = 0;
     const auto header_offset = reserve_words(cursor, 1);
     const auto locations_offset = reserve_words(cursor, m);
     const auto requests_offset = reserve_words(cursor, m);
     const auto positions_offset = reserve_words(cursor, m);
-    const auto mapping_offset = reserve_words(cursor, mapping.numel());
+    const auto row_context_offset = reserve_words(cursor, m);
     std::vector<int32_t> words(cursor, 0);
     words[header_offset] = static_cast<int32_t>(m);
     std::copy(locations_h_.begin(), locations_h_.end(), words.begin() + locations_offset);
     std::copy(requests_h_.begin(), requests_h_.end(), words.begin() + requests_offset);
     std::copy(positions_h_.begin(), positions_h_.end(), words.begin() + positions_offset);
-    std::copy(mapping_h_.begin(), mapping_h_.end(), words.begin() + mapping_offset);
+    for (int64_t i = 0; i < m; ++i) words[row_context_offset + i] = positions_h_[i] + 1;
     storage_ = upload_words(words, cursor);
     header_ = storage_.narrow(0, header_offset, 1);
     locations_ = storage_.narrow(0, locations_offset, m);
     requests_ = storage_.narrow(0, requests_offset, m);
     positions_ = storage_.narrow(0, positions_offset, m);
-    mapping_ = storage_.narrow(0, mapping_offset, mapping.numel()).view({request_count, context});
+    row_context_ = storage_.narrow(0, row_context_offset, m);
   }
 
   // Device constructor. Sequence s covers the next lengths[s] rows at
@@ -397,6 +461,7 @@ class PagedMetadata : public torch::CustomClassHolder {
     const auto prefix_offset = reserve_words(words, batch);
     const auto first_offset = reserve_words(words, batch);
     const auto visible_offset = reserve_words(words, 2 * batch);
+    const auto row_context_offset = reserve_words(words, m);
     const auto model_offset = positions_on_cpu ? reserve_words(words, 2 * m) : 0;
     const auto staged_words = words;
     const auto locations_offset = reserve_words(words, bucket);
@@ -407,6 +472,7 @@ class PagedMetadata : public torch::CustomClassHolder {
     const auto status_offset = scheduler_owned ? 0 : reserve_words(words, 2 * bucket + 1);
     std::vector<int32_t> host(staged_words, 0);
     host[header_offset] = static_cast<int32_t>(m);
+    for (int64_t i = 0; i < m; ++i) host[row_context_offset + i] = positions_h_[i] + 1;
     std::copy(last.begin(), last.end(), host.begin() + last_offset);
     std::copy(row_seq.begin(), row_seq.end(), host.begin() + row_seq_offset);
     std::copy(seq_prefix.begin(), seq_prefix.end(), host.begin() + prefix_offset);
@@ -420,6 +486,7 @@ class PagedMetadata : public torch::CustomClassHolder {
     locations_ = storage_.narrow(0, locations_offset, m);
     requests_ = storage_.narrow(0, requests_offset, m);
     positions_ = storage_.narrow(0, positions_offset, m);
+    row_context_ = storage_.narrow(0, row_context_offset, m);
     if (has_tokens) token_ids_ = storage_.narrow(0, tokens_offset, m);
     if (positions_on_cpu)
       model_positions_ = storage_.narrow(0, model_offset, 2 * m).view(at::kLong);
@@ -535,7 +602,7 @@ class PagedMetadata : public torch::CustomClassHolder {
   at::Tensor rotary_header() const { return header_; }
   at::Tensor row_locations() const { return locations_; }
   at::Tensor row_requests() const { return requests_; }
-  at::Tensor request_mapping() const { return mapping_; }
+  at::Tensor request_mapping() { return device_mapping(); }
   at::Tensor model_positions() const {
     TORCH_CHECK(model_positions_.defined(), "GaudiRT: model positions require fused scheduler metadata");
     return model_positions_;
@@ -589,7 +656,7 @@ class PagedMetadata : public torch::CustomClassHolder {
     // visible token t of every request sits at mapping[r, t - t % P] + t % P
     // with a P-aligned page start; P = 1 keeps the token-granular map.
     const bool host_map = !mapping_h_.empty();
-    const int64_t page = host_map ? page_size() : page_;
+    const int64_t page = page_;
     const int64_t max_pages = std::max<int64_t>(1, (context_ + page - 1) / page);
     // Split the rows: runs of >= kPrefillMinRows consecutive positions become
     // prefill sequences (MFMA tiles of rows x heads) when the prefill kernel
@@ -622,6 +689,17 @@ class PagedMetadata : public torch::CustomClassHolder {
       return offset;
     };
     info->decode_rows = static_cast<int64_t>(dec_map.size());
+    // Every row a decode row, in batch order (a serving decode step): the
+    // decode kernel reads the metadata's row requests directly.
+    bool all_decode = info->decode_rows == rows_;
+    for (int64_t i = 0; all_decode && i < info->decode_rows; ++i) all_decode = dec_map[i] == i;
+    if (all_decode) {
+      info->row_request_ref = requests_;
+      info->row_context_ref = row_context_;
+      dec_request.clear();
+      dec_context.clear();
+      dec_map.clear();
+    }
     info->row_request_offset = append(dec_request);
     info->row_context_offset = append(dec_context);
     info->row_map_offset = append(dec_map);
@@ -630,8 +708,11 @@ class PagedMetadata : public torch::CustomClassHolder {
     info->seq_first_row_offset = append(seq_first);
     info->seq_rows_offset = append(seq_rows);
     info->seq_prefix_offset = append(seq_prefix);
+    // Page 1: the request map itself is the block table, read in place.
     std::vector<int32_t> tables;
-    if (host_map) {
+    if (page == 1) {
+      info->block_tables_ref = device_mapping();
+    } else if (host_map) {
       tables.assign(request_count_ * max_pages, -1);
       for (int64_t r = 0; r < request_count_; ++r)
         for (int64_t t = 0; t <= max_position_[r]; t += page)
@@ -639,22 +720,24 @@ class PagedMetadata : public torch::CustomClassHolder {
     }
     info->block_table_offset = append(tables);
     while (words.size() % 4) words.push_back(0);
-    const int64_t total = host_map ? static_cast<int64_t>(words.size()) : info->block_table_offset + request_count_ * max_pages;
+    const int64_t total = host_map || page == 1 ? static_cast<int64_t>(words.size())
+                                                : info->block_table_offset + request_count_ * max_pages;
     info->block_size = page;
     info->bt_stride = max_pages;
-    info->storage = upload_words(words, total);
+    // A plan whose sections are all read in place (a decode step over the
+    // token-granular map) keeps the metadata's row contexts as its storage:
+    // no allocation and no copy.
+    info->storage = total == 0 && all_decode ? row_context_ : upload_words(words, total);
     if (!host_map) {
       auto& storage = info->storage;
       const auto section = [&](int64_t offset, int64_t count) { return storage.narrow(0, offset, count); };
-      if (info->decode_rows)
+      if (info->decode_rows && !all_decode)
         section(info->row_request_offset, info->decode_rows)
             .copy_(requests_.index_select(0, section(info->row_map_offset, info->decode_rows)));
       if (info->prefill_seqs)
         section(info->seq_request_offset, info->prefill_seqs)
             .copy_(requests_.index_select(0, section(info->seq_first_row_offset, info->prefill_seqs)));
-      if (page == 1)
-        section(info->block_table_offset, request_count_ * context_).copy_(mapping_.reshape({-1}));
-      else
+      if (page != 1)
         check_gk(gk_block_tables(mapping_.data_ptr<int32_t>(), static_cast<int32_t>(request_count_),
                                  static_cast<int32_t>(context_), static_cast<int32_t>(page),
                                  storage.data_ptr<int32_t>() + info->block_table_offset,
@@ -671,26 +754,21 @@ class PagedMetadata : public torch::CustomClassHolder {
     int32_t row, length, prefix;
   };
 
-  int64_t page_size() const {
-    for (int64_t page = 1024; page > 1; page >>= 1) {
-      bool ok = true;
-      for (int64_t r = 0; r < request_count_ && ok; ++r) {
-        const int32_t* map = mapping_h_.data() + r * context_;
-        for (int64_t t = 0; t <= max_position_[r] && ok; ++t) {
-          const int64_t start = t - t % page;
-          ok = map[start] % page == 0 && map[t] == map[start] + t % page;
-        }
-      }
-      if (ok) return page;
-    }
-    return 1;
+  // The request map on the device: the device constructors' own input, or
+  // (host constructor) the host copy, uploaded on the current stream on first use.
+  const at::Tensor& device_mapping() {
+    if (!mapping_.defined()) mapping_ = upload_words(mapping_h_, request_count_ * context_).view({request_count_, context_});
+    return mapping_;
   }
 
   int64_t rows_ = 0, slots_ = 0, request_count_ = 0, context_ = 0, vocabulary_ = 0, page_ = 1;
   // Host copies (host constructor only; device metadata keeps positions_h_).
   std::vector<int32_t> locations_h_, requests_h_, positions_h_, mapping_h_, max_position_;
   std::vector<Sequence> sequences_;
-  at::Tensor storage_, locations_, requests_, positions_, mapping_, header_, token_ids_, last_token_indices_,
+  // row_context_: visible keys of each row (its position + 1), the decode
+  // kernel's row_context when every row is a decode row.
+  at::Tensor storage_, locations_, requests_, positions_, row_context_, mapping_, header_, token_ids_,
+      last_token_indices_,
       model_positions_;
   std::unordered_map<int64_t, at::Tensor> plans_;
 };
@@ -818,7 +896,7 @@ at::Tensor paged_attn_impl(const at::Tensor& query, const at::Tensor& key, const
     f.q_row_stride = q.stride(0);
     f.pool = pool;
     f.slots = plan.slots;
-    f.block_tables = words + plan.block_table_offset;
+    f.block_tables = plan.block_tables(words);
     f.bt_stride = plan.bt_stride;
     f.block_size = static_cast<int32_t>(plan.block_size);
     f.seq_request = words + plan.seq_request_offset;
@@ -844,12 +922,12 @@ at::Tensor paged_attn_impl(const at::Tensor& query, const at::Tensor& key, const
     p.q_row_stride = q.stride(0);
     p.pool = pool;
     p.slots = plan.slots;
-    p.block_tables = words + plan.block_table_offset;
+    p.block_tables = plan.block_tables(words);
     p.bt_stride = plan.bt_stride;
     p.block_size = static_cast<int32_t>(plan.block_size);
-    p.row_request = words + plan.row_request_offset;
-    p.row_context = words + plan.row_context_offset;
-    p.row_map = words + plan.row_map_offset;
+    p.row_request = plan.row_request(words);
+    p.row_context = plan.row_context(words);
+    p.row_map = plan.row_map(words);
     p.rows = static_cast<int32_t>(plan.decode_rows);
     p.q_heads = static_cast<int32_t>(plan.query_heads);
     p.kv_heads = static_cast<int32_t>(plan.kv_heads);
@@ -858,6 +936,7 @@ at::Tensor paged_attn_impl(const at::Tensor& query, const at::Tensor& key, const
     p.softcap = softcap_f;
     p.sliding_window = sw;
     p.max_context = static_cast<int32_t>(plan.decode_max_context);
+    p.partition_tokens = g_decode_partition.load(std::memory_order_relaxed);
     p.out = output.data_ptr();
     p.out_row_stride = output.stride(0);
     const size_t need = gk_paged_decode_workspace_bytes(&p);
@@ -1188,7 +1267,19 @@ TORCH_LIBRARY_IMPL(gaudirt, CUDA, m) {
   m.impl("rotary_paged_attn", TORCH_FN(gaudirt_amd::rotary_paged_attn));
 }
 
+namespace gaudirt_amd {
+void set_decode_partition(int64_t tokens) {
+  TORCH_CHECK(tokens >= 0 && tokens <= 8192 && tokens % 32 == 0,
+              "GaudiRT: the decode partition must be 0 (library choice) or a multiple of 32 keys up to 8192");
+  g_decode_partition.store(static_cast<int32_t>(tokens), std::memory_order_relaxed);
+}
+int64_t decode_partition() { return g_decode_partition.load(std::memory_order_relaxed); }
+}  // namespace gaudirt_amd
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("_set_decode_partition", &gaudirt_amd::set_decode_partition,
+        "split-K partition of paged_attn's decode rows (0: library choice; > 0: fixed, batch-invariant)");
+  m.def("_decode_partition", &gaudirt_amd::decode_partition);
   m.def("_allocate_paged_kv", &gaudirt_amd::allocate_paged_kv, "zeroed head-major bf16 KV pool");
   m.def("_allocate_paged_slots", &gaudirt_amd::allocate_paged_slots, "page-granular KV slots for new tokens");
   m.def("_release_paged_slots", &gaudirt_amd::release_paged_slots, "distinct pages of released KV slots");

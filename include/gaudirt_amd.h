@@ -90,7 +90,10 @@ typedef struct gk_decode_params {
   int32_t partition_tokens;    /* split-K partition (multiple of 32); 0 = library choice: for
                                   GQA groups >= 4 (any block_size) a balanced split of all
                                   key tiles over one resident grid, otherwise a partition
-                                  sized from the batch */
+                                  sized from the batch; either way a row's split points,
+                                  and so its last bits, depend on the whole batch. A fixed
+                                  partition (> 0) makes every row's output a function of
+                                  that row alone, bit for bit (batch-invariant decode) */
   void* out;                   /* bf16 [rows, out_row_stride] */
   int64_t out_row_stride;      /* elements */
   /* Optional fused KV store of the new token rows (NULL new_key = none): written

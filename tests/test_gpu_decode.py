@@ -141,3 +141,28 @@ def test_c3_fused_store_then_decode(runner):
                                before[kind, h][~touched].view(torch.int16)), (kind, h)
     del before
     check_against_oracle(cases.host_case(dc), runner.bits_of(dc.out), flat=True)
+
+
+@pytest.mark.parametrize("geometry,partition", [((32, 8, 128), 512), ((32, 8, 128), 2048), ((16, 8, 128), 1024),
+                                                ((64, 8, 128), 2048)])
+def test_fixed_partition_rows_do_not_depend_on_the_batch(runner, geometry, partition):
+    # With a fixed partition every row's output is a function of that row
+    # alone: the same bits when the row runs alone, or in the batch in reverse
+    # order. Rows span up to several partitions (split-K merge per row), GQA 2
+    # takes the dot2 kernel, 4 and 8 the MFMA kernel.
+    import copy
+
+    heads, kv_heads, d = geometry
+    rng = np.random.default_rng(partition + heads)
+    lens = np.concatenate([[1, partition, partition + 1, 3 * partition + 7], rng.integers(1, 4 * partition, 12)])
+    case = cases.decode_case(partition + heads, len(lens), heads, kv_heads, d, 128, 1024, lens)
+    batch = runner.run_case(case, partition=partition)
+    check_against_oracle(case, batch)
+    order = np.arange(len(lens))[::-1]
+    rev = copy.copy(case)
+    rev.query, rev.block_tables, rev.lens = case.query[order], case.block_tables[order], case.lens[order]
+    assert np.array_equal(runner.run_case(rev, partition=partition), batch[order])
+    for r in (0, 2, 3, 9):
+        one = copy.copy(case)
+        one.query, one.block_tables, one.lens = case.query[r:r + 1], case.block_tables[r:r + 1], case.lens[r:r + 1]
+        assert np.array_equal(runner.run_case(one, partition=partition), batch[r:r + 1]), r

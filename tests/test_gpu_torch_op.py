@@ -150,6 +150,63 @@ def test_single_row_replay_matches_batch(torch_ext):
     del gaudirt_amd
 
 
+@pytest.fixture
+def batch_invariant(torch_ext):
+    import gaudirt_amd
+
+    gaudirt_amd.set_batch_invariant_decode(True)
+    assert gaudirt_amd.batch_invariant_decode() == gaudirt_amd.BATCH_INVARIANT_PARTITION
+    yield gaudirt_amd.BATCH_INVARIANT_PARTITION
+    gaudirt_amd.set_batch_invariant_decode(False)
+    assert gaudirt_amd.batch_invariant_decode() == 0
+
+
+def replay_rows(torch, results, meta_rows, scale, heads, dim):
+    """paged_attn on each listed row alone (its own one-row metadata); the bits of each output."""
+    actual, problem, out, (q, k, v, key_pool, value_pool) = results[0]
+    mapping = torch.from_numpy(problem.mapping)
+    got = []
+    for r in meta_rows:
+        requests = torch.from_numpy(problem.requests[r:r + 1].copy())
+        positions = torch.from_numpy(problem.positions[r:r + 1].copy())
+        locations = mapping[requests, positions].to(torch.int64)
+        one = torch.classes.gaudirt.PagedMetadata(locations, requests, positions, mapping, problem.slots)
+        replay = torch.ops.gaudirt.paged_attn.default(q[r:r + 1], k[r:r + 1], v[r:r + 1], key_pool, value_pool, one,
+                                                      dim, scale)
+        got.append(bits(replay))
+    return got
+
+
+def test_single_row_replay_is_bitwise_in_batch_invariant_mode(torch_ext, batch_invariant):
+    # tests/paged_attention_smoke.py:145-150 as the reference asserts it: the
+    # last row of the 137-row batch replayed alone equals the batched row bit
+    # for bit, here with the decode rows on fixed partitions.
+    torch = torch_ext
+    results, meta, scale = run_case(torch, 56, 8, 128, 64, 32, 137)
+    actual, problem = results[0][0], results[0][1]
+    check(actual, problem)
+    (replay,) = replay_rows(torch, results, [136], scale, 56, 128)
+    assert np.array_equal(replay, actual[-1:])
+
+
+def test_long_rows_are_batch_invariant_in_batch_invariant_mode(torch_ext, batch_invariant):
+    # Rows of up to 6000 keys span several fixed partitions (a split-K merge per
+    # row); each replayed alone must equal its batched bits, and the batch must
+    # still pass the parity gate.
+    torch = torch_ext
+    rng = np.random.default_rng(2026)
+    requests_n, context = 24, 6000
+    positions = torch.from_numpy(rng.integers(1, context, requests_n).astype(np.int64))
+    positions[:3] = torch.tensor([context - 1, batch_invariant, batch_invariant - 1])
+    results, meta, scale = run_case(torch, 32, 8, 128, requests_n, context, requests_n, positions=positions,
+                                    request_ids=torch.arange(requests_n, dtype=torch.int64))
+    actual, problem = results[0][0], results[0][1]
+    print("max/mean abs", check(actual, problem), flush=True)
+    rows = [0, 1, 2, 5, 11, 23]
+    for r, replay in zip(rows, replay_rows(torch, results, rows, scale, 32, 128)):
+        assert np.array_equal(replay, actual[r:r + 1]), r
+
+
 @pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("position", [254, 255, 511])
 def test_gqa_geometry(torch_ext, dim, position):
