@@ -26,8 +26,12 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # some of their forms have given wrong results without an error on this part.
 # The host pass warns that it does not know the feature.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Tuning variants of the kernels as extra -D flags, e.g.
+# GAUDIRT_AMD_DEFINES="-DGK_PREFILL_MFMA32=1" (the 32 x 32 prefill variant);
+# empty for the shipping build.
+DEFINES = os.environ.get("GAUDIRT_AMD_DEFINES", "").split()
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", str(ROOT / "include"), "-I", str(CSRC),
-          "-Wall", "-Wno-unused-function"]
+          "-Wall", "-Wno-unused-function", *DEFINES]
 
 LIB_SOURCES = ["gk_api.cpp", "block_allocator_core.cpp", "block_allocator.cpp", "kv_store.hip", "paged_decode.hip", "decode_stream.hip",
                "paged_prefill.hip", "metadata.hip", "rotary.hip"]

@@ -607,10 +607,382 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   }
 }
 
+// ---------------------------------------------------------------------------
+// head_dim 128 on 32 x 32 tiles (v_mfma_f32_32x32x16_bf16)
+// ---------------------------------------------------------------------------
+// An opt-in build variant (GK_PREFILL_MFMA32=1), not the shipping form: on C4
+// it ran 147.5 us against 135.5 us for prefill_kernel (same box). Its
+// counters show less of every instruction class but 52% more wave-cycles
+// waiting: with one 32-row tile per wave each K operand read feeds a single
+// 32-cycle MFMA, and at ~250 VGPRs (two waves per SIMD) the compiler cannot
+// keep reads in flight ahead of their MFMAs. The same work item, pipeline
+// and numerics as prefill_kernel, with each wave's 32 query rows as one
+// 32-column tile:
+//   S^T[key][qrow] = K . Q^T      per 32-key group, 8 MFMAs over 16-dim chunks
+//   O^T[dim][qrow] += V^T . P^T   per 32-dim block, 4 MFMAs over 16-key chunks
+// Output lane l holds column l % 32 of both products: all 32 scores of one
+// step and all 64 accumulator values of the lane's query row (half the keys
+// and dims; lane l + 32 holds the rest of the same row). The probabilities are
+// the B operand of P.V straight from the score registers, re-basing scales a
+// lane's own registers, and a row's maximum and sum combine the two halves
+// with one 32-lane swap. Against 16 x 16 tiles: half the MFMA issues per step,
+// no cross-lane moves of the re-base factors, and the row sums on the VALU
+// (v_dot2 of the bf16 probabilities with ones) instead of four MFMAs.
+//
+// Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on the GPU with an
+// in-bounds probe): A row l % 32 and B column l % 32 hold k slots
+// 8 (l / 32) .. + 7; D register r of lane l is row 8 (r / 4) + 4 (l / 32) +
+// r % 4, column l % 32.
+//
+// LDS token swizzle swz32 (16-byte chunk c of token t stored at c ^ swz32(t)):
+//  - K operand reads (ds_read_b128, 32 lanes at a time over 128 banks, two
+//    256-byte rows per bank row): the 32 tokens of a key group read one
+//    logical chunk, so swz32 must be a bijection of bits 1-4 of t for each t0;
+//  - V^T reads (ds_read_b64_tr_b16, 32 lanes over 64 banks): 4 consecutive
+//    tokens (aligned) x an aligned group of 4 chunks, so bits 2-3 of swz32 must
+//    be a bijection of (t0, t1).
+// swz32 = t1 << 3 | (t0 ^ t2) << 2 | t3 << 1 | t4 meets both.
+__device__ __forceinline__ int swz32(int t) {
+  return ((t & 2) << 2) | (((t ^ (t >> 2)) & 1) << 2) | ((t & 8) >> 2) | ((t >> 4) & 1);
+}
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x16_t mfma32x32(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <bool SOFTCAP, int MODE>
+__global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill32_kernel(PrefillArgs a) {
+  constexpr int D = 128;
+  using S = PrefillShape<D>;
+  constexpr int kKeys = 64;        // keys per step: two 32-key groups
+  constexpr int NC = D / 16;       // 16-dim k chunks of Q.K
+  constexpr int NB = D / 32;       // 32-dim blocks of P.V
+  constexpr int KC = kKeys / 16;   // 16-key k chunks of P.V
+  static_assert(S::TILE == kKeys * D * 2, "tile of a 64-key step");
+  constexpr int LPW = (S::NI + kPrefillWaves - 1) / kPrefillWaves;
+  constexpr int NE = MODE == kStepBlocks ? 1 : LPW;
+  constexpr int KPL = kKeys / S::NI;
+  constexpr bool CLAMPED = MODE != kStepBlocks;
+  constexpr int kOutRowBytes = 2 * D + 16;
+  constexpr int kKvBytes = 2 * 2 * S::TILE, kOutBytes = kPrefillWaves * kQrowsPerWave * kOutRowBytes;
+  static_assert(kQrowsPerWave == 32, "one 32-column tile per wave");
+  __shared__ __attribute__((aligned(16))) char lds[kKvBytes + kOutBytes];
+  auto kv = reinterpret_cast<char(*)[2][S::TILE]>(lds);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hf = lane >> 5, col = lane & 31;  // half (k slots / output rows) and column of the 32 x 32 tiles
+  // Work item and prologue: as prefill_kernel.
+  asm volatile("" ::"s"(a.seq_rows), "s"(a.seq_prefix), "s"(a.seq_first_row), "s"(a.seq_request),
+               "s"(a.block_tables), "s"(a.query), "s"(a.pool), "s"(a.out), "s"(a.tiles), "s"(a.seqs),
+               "s"(a.rows_per_tile), "s"(a.group), "s"(a.bt_stride), "s"(a.block_shift), "s"(a.window),
+               "s"(a.q_stride), "s"(a.slots), "s"(a.kv_heads), "s"(gridDim.x), "s"(a.tiles_div.mul),
+               "s"(a.tiles_div.shift), "s"(a.seqs_div.mul), "s"(a.seqs_div.shift), "s"(a.group_div.mul),
+               "s"(a.group_div.shift));
+  const int nitems = gridDim.x, xcd = blockIdx.x % kXcds, per_xcd = nitems / kXcds, extra = nitems % kXcds;
+  const auto div_tiles = [&](int x) { return (int)fast_div((uint32_t)x, a.tiles_div); };
+  const auto div_group = [&](int x) { return (int)fast_div((uint32_t)x, a.group_div); };
+  const int item = heavy_first_item(xcd * per_xcd + min(xcd, extra), per_xcd + (xcd < extra), a.tiles,
+                                    (int)blockIdx.x / kXcds, div_tiles);
+  const int item_seq = div_tiles(item), tile = item - item_seq * a.tiles;
+  const int kvh = (int)fast_div((uint32_t)item_seq, a.seqs_div), seq = item_seq - kvh * a.seqs;
+  const int rows = a.seq_rows[seq], prefix = a.seq_prefix[seq], seq_first = a.seq_first_row[seq];
+  const int request = a.seq_request[seq];
+  asm volatile("" ::"s"(rows), "s"(prefix), "s"(seq_first), "s"(request));
+  const int r0 = tile * a.rows_per_tile;
+  if (r0 >= rows) return;
+  const int nr = min(a.rows_per_tile, rows - r0);
+  const int first_row = seq_first + r0;
+  const int32_t* __restrict__ bt = a.block_tables + (int64_t)request * a.bt_stride;
+  const int g = a.group;
+  const int pos_lo = prefix + r0, pos_hi = prefix + r0 + nr - 1;
+  const int key_end = pos_hi + 1;
+  const int key_begin = a.window > 0 ? max(0, pos_lo - a.window + 1) : 0;
+  const int kb0 = key_begin & ~(kKeys - 1);
+  const int nsteps = (key_end - kb0 + kKeys - 1) / kKeys;
+
+  // This lane's query row qrow = (row, head), column `col` of the wave's tile.
+  const int qr = wave * kQrowsPerWave + col;
+  const int qrow_row = div_group(qr), qrow_head = qr - qrow_row * g;
+  const bool qvalid = qrow_row < nr;
+  const int qpos = qvalid ? pos_lo + qrow_row : -1;
+  const int qleft = a.window > 0 ? qpos - a.window + 1 : 0;
+  // Q^T as the B operand of S^T = K . Q^T: k chunk c holds dims 16 c + 8 hf .. + 7.
+  bf16x8_t qb[NC];
+  {
+    const uint16_t* src =
+        a.query + (int64_t)(first_row + qrow_row) * a.q_stride + (int64_t)(kvh * g + qrow_head) * D + 8 * hf;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (qvalid) v = load16(src + 16 * c);
+      qb[c] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+  const int wave_pos_min = pos_lo + div_group(wave * kQrowsPerWave);
+  const int wave_left_max =
+      a.window > 0 ? pos_lo + min(nr - 1, div_group(wave * kQrowsPerWave + kQrowsPerWave - 1)) - a.window + 1 : 0;
+
+  f32x16_t o[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) o[b] = f32x16_t{};
+  // Running maximum (log2 units), its re-base threshold on raw scores, the
+  // probability base (m_run, or 0 before the first maximum) and this lane's
+  // share of the row sum (its half of the keys).
+  float m_run = -INFINITY, m_thr = -INFINITY, m_base = 0.f, l_run = 0.f;
+  const float inv_scale = 1.f / a.score_scale;
+
+  const uint16_t* kbase = a.pool + (int64_t)kvh * a.slots * D;
+  const uint16_t* vbase = kbase + (int64_t)a.kv_heads * a.slots * D;
+  const uint32_t region = (uint32_t)(a.slots * D * 2);
+  const u32x4_t krs = buffer_words(kbase, region), vrs = buffer_words(vbase, region);
+  const int shift = a.block_shift, bmask = (1 << shift) - 1;
+
+  struct Entries {
+    int e[NE];
+  };
+  auto entry_of = [&](int tb) __attribute__((always_inline)) {
+    Entries en;
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      int key = tb;
+      if constexpr (MODE == kLoadBlocks) key += (wave + k * kPrefillWaves) * KPL;
+      if constexpr (MODE == kKeyBlocks) key += (wave + k * kPrefillWaves) * KPL + lane / S::CPR;
+      if constexpr (CLAMPED) key = min(max(key, key_begin), key_end - 1);
+      if constexpr (MODE == kKeyBlocks) en.e[k] = bt[key >> shift];
+      else en.e[k] = scalar_load(bt, key >> shift);
+    }
+    return en;
+  };
+  // Direct-load offsets as in prefill_kernel, with the swz32 token swizzle.
+  struct Offsets {
+    uint32_t v[LPW];
+  };
+  auto offsets_of = [&](int tb, const Entries& en) __attribute__((always_inline)) {
+    Offsets of{};
+    const int lo = key_begin - tb, hi = key_end - 1 - tb;
+    const uint32_t step_slot = ((uint32_t)en.e[0] << shift) + (uint32_t)(tb & bmask);
+#pragma unroll
+    for (int k = 0; k < LPW; ++k) {
+      const int ins = wave + k * kPrefillWaves;
+      if (S::NI % kPrefillWaves != 0 && ins >= S::NI) break;
+      const int p = ins * 64 + lane, tt = p / S::CPR, pc = p % S::CPR;
+      uint32_t slot;
+      if constexpr (MODE == kStepBlocks) {
+        slot = step_slot + (uint32_t)min(max(tt, lo), hi);
+      } else {
+        const int key = min(max(tb + tt, key_begin), key_end - 1);
+        slot = (uint32_t)((en.e[k] << shift) | (key & bmask));
+      }
+      of.v[k] = slot * (2 * D) + ((pc ^ swz32(tt)) << 4);
+    }
+    return of;
+  };
+  auto issue = [&](const Offsets& of, u32x4_t rs, char* t) __attribute__((always_inline)) {
+    if constexpr (MODE == kKeyBlocks) wait_vmem_visible();
+    const uint32_t base = lds_addr(t);
+#pragma unroll
+    for (int k = 0; k < LPW; ++k) {
+      const int ins = wave + k * kPrefillWaves;
+      if (S::NI % kPrefillWaves != 0 && ins >= S::NI) break;
+      lds_dma16_w(base + ins * 1024, rs, of.v[k]);
+    }
+  };
+
+  f32x16_t sc[2];        // scores of the step's two key groups
+  bf16x8_t pa[KC];       // probabilities: B operand of k chunk kc (keys 16 kc .. + 15)
+
+  // S^T = K . Q^T: group kg's scores in sc[kg]; lane (hf, col) reads token
+  // 32 kg + col, logical chunk 2 c + hf.
+  auto scores = [&](const char* kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kg = 0; kg < 2; ++kg) {
+      sc[kg] = f32x16_t{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const bf16x8_t kr = *reinterpret_cast<const bf16x8_t*>(kt + (32 * kg + col) * (2 * D) +
+                                                              (((2 * c + hf) ^ swz32(col)) << 4));
+        sc[kg] = mfma32x32(kr, qb[c], sc[kg]);
+      }
+    }
+  };
+  // V^T operand of k chunk kc, dim block b: lane (hf, col) gets dim 32 b + col
+  // at keys 16 kc + 4 hf + (0..3) and 16 kc + 8 + 4 hf + (0..3); each 16-lane
+  // group reads 4 consecutive keys x 16 dims transposed.
+  auto read_v = [&](const char* vt, int kc, int b) __attribute__((always_inline)) {
+    const int i = lane & 15, gb = (lane >> 4) & 1;
+    const int lc = 4 * b + 2 * gb + ((i & 3) >> 1);
+    const int t0 = 16 * kc + 4 * hf + (i >> 2), t1 = t0 + 8;
+    const bf16x4_t v0 = lds_read_tr4(vt + t0 * (2 * D) + ((lc ^ swz32(t0)) << 4) + ((i & 1) << 3));
+    const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz32(t1)) << 4) + ((i & 1) << 3));
+    return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  auto accumulate = [&](const char* vt, const bf16x8_t* vfirst) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const bf16x8_t v = (kc == 0 && vfirst) ? vfirst[b] : read_v(vt, kc, b);
+        o[b] = mfma32x32(v, pa[kc], o[b]);
+      }
+  };
+
+  // Online softmax of the step at tb. Score register r of group kg is key
+  // tb + 32 kg + 8 (r / 4) + 4 hf + r % 4 of this lane's query row.
+  auto softmax = [&](int tb) __attribute__((always_inline)) {
+    const bool full = !SOFTCAP && tb + kKeys - 1 <= wave_pos_min && tb >= wave_left_max;
+    if constexpr (SOFTCAP) {
+#pragma unroll
+      for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = tb + 32 * kg + 8 * (r >> 2) + 4 * hf + (r & 3);
+          const float sv = a.softcap_log2 * soft_tanh(sc[kg][r] * a.score_scale);
+          sc[kg][r] = (key <= qpos && key >= qleft) ? sv : -INFINITY;
+        }
+    } else if (!full) {
+#pragma unroll
+      for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = tb + 32 * kg + 8 * (r >> 2) + 4 * hf + (r & 3);
+          sc[kg][r] = (key <= qpos && key >= qleft) ? sc[kg][r] : -INFINITY;
+        }
+    }
+    float t[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) t[i] = sc[i >> 4][i & 15];
+    float mx = tree_max(t);
+    // Probabilities against the current base right away (as prefill_kernel);
+    // the cross-half maximum only decides afterwards whether to re-base.
+    auto probabilities = [&](float base) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        float ps;
+        if constexpr (SOFTCAP) ps = fast_exp2(sc[i >> 4][i & 15] - base);
+        else ps = fast_exp2(__builtin_fmaf(sc[i >> 4][i & 15], a.score_scale, -base));
+        pa[i >> 3][i & 7] = (__bf16)ps;
+      }
+    };
+    probabilities(m_base);
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const auto w = __builtin_bit_cast(u32x4_t, pa[kc]);
+      asm volatile("" ::"v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]));
+    }
+    {
+      const auto h2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = max2(__uint_as_float(h2[0]), __uint_as_float(h2[1]));
+    }
+    if (__builtin_amdgcn_ballot_w64(mx > (SOFTCAP ? m_run + kLazyRescale : m_thr))) {
+      if (mx > (SOFTCAP ? m_run + kLazyRescale : m_thr)) {
+        const float m_new = fmaxf(m_run, SOFTCAP ? mx : mx * a.score_scale);
+        const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
+        m_run = m_new;
+        m_thr = (m_new + kLazyRescale) * inv_scale;
+        m_base = m_new == -INFINITY ? 0.f : m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) o[b] *= alpha;
+      }
+      probabilities(m_base);
+    }
+    // This lane's share of the row sum: the bf16 probabilities, in pairs.
+    const bf16x2_t ones = {(__bf16)1.f, (__bf16)1.f};
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bf16x2_t pair = {pa[kc][2 * u], pa[kc][2 * u + 1]};
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l_run, false);
+      }
+  };
+
+  {
+    Entries e_next{};
+    {
+      const Offsets first = offsets_of(kb0, entry_of(kb0));
+      issue(first, krs, kv[0][0]);
+      issue(first, vrs, kv[0][1]);
+    }
+    if (1 < nsteps) e_next = entry_of(kb0 + kKeys);
+    auto body = [&](int step, auto stage) __attribute__((always_inline)) {
+      constexpr int cur = decltype(stage)::value, next = cur ^ 1;
+      const int tb = kb0 + step * kKeys;
+      wait_vmem<0>();
+      __syncthreads();
+      wait_vmem_visible();
+      if (step + 1 < nsteps) {
+        const Offsets of = offsets_of(tb + kKeys, e_next);
+        issue(of, krs, kv[next][0]);
+        issue(of, vrs, kv[next][1]);
+        if (step + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
+      }
+      scores(kv[cur][0]);
+      bf16x8_t vfirst[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) vfirst[b] = read_v(kv[cur][1], 0, b);
+      softmax(tb);
+      accumulate(kv[cur][1], vfirst);
+    };
+    int step = 0;
+    for (; step + 1 < nsteps; step += 2) {
+      body(step, std::integral_constant<int, 0>{});
+      body(step + 1, std::integral_constant<int, 1>{});
+    }
+    if (step < nsteps) body(step, std::integral_constant<int, 0>{});
+  }
+
+  // Normalise: the row sum is this lane's share plus lane (col + 32)'s; the
+  // lane's dims 32 b + 8 u + 4 hf + (0..3) go to its row in LDS as 8-byte
+  // pieces, then each wave stores its rows as 16-byte pieces.
+  {
+    const auto h2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    const float l = __uint_as_float(h2[0]) + __uint_as_float(h2[1]);
+    const float inv = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
+    char* row_lds = lds + kKvBytes + (wave * kQrowsPerWave + col) * kOutRowBytes;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        bf16x4_t w;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) w[v] = (__bf16)(o[b][4 * u + v] * inv);
+        *reinterpret_cast<bf16x4_t*>(row_lds + (32 * b + 8 * u + 4 * hf) * 2) = w;
+      }
+  }
+  char* rows_lds = lds + kKvBytes + wave * kQrowsPerWave * kOutRowBytes;
+  constexpr int kPieces = kQrowsPerWave * D / 8;
+#pragma unroll
+  for (int i = 0; i < kPieces / 64; ++i) {
+    const int piece = i * 64 + lane, ql = piece / (D / 8), part = piece % (D / 8);
+    const int qrr = wave * kQrowsPerWave + ql;
+    const int row = div_group(qrr), head = qrr - row * g;
+    const uint4 v = *reinterpret_cast<const uint4*>(rows_lds + ql * kOutRowBytes + part * 16);
+    if (row < nr)
+      *reinterpret_cast<uint4*>(a.out + (int64_t)(first_row + row) * a.out_stride + (int64_t)(kvh * g + head) * D +
+                                part * 8) = v;
+  }
+}
+
+// Head_dim 128 on 16 x 16 tiles with prefill_kernel (0, shipping) or on 32 x 32
+// tiles with prefill32_kernel (1, a build variant kept for its measurement).
+#ifndef GK_PREFILL_MFMA32
+#define GK_PREFILL_MFMA32 0
+#endif
+
 template <int D, int MODE>
 void launch_mode(const PrefillArgs& a, bool softcap, dim3 grid, hipStream_t stream) {
-  if (softcap) prefill_kernel<D, true, MODE><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
-  else prefill_kernel<D, false, MODE><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+  if constexpr (D == 128 && GK_PREFILL_MFMA32) {
+    if (softcap) prefill32_kernel<true, MODE><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+    else prefill32_kernel<false, MODE><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+  } else {
+    if (softcap) prefill_kernel<D, true, MODE><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+    else prefill_kernel<D, false, MODE><<<grid, kPrefillWaves * 64, 0, stream>>>(a);
+  }
 }
 
 template <int D>
