@@ -15,8 +15,8 @@ restatement of the reference's direct_bf16_pv, on the host's cores). With the
 default headline workload (c2) the same line carries `secondary`: the other
 GPU configurations (c3 fused store + decode, c5 long-context decode: HBM
 roofline; c4 prefix-shared prefill: MFMA roofline), each timed the same way in
-the same process after the headline, `--steps` steps each (c3 and c5 after at
-least 20 warm-up steps, c4 after 1000).
+the same process right after the headline, `--steps` steps each (c3 and c5
+after at least 100 warm-up steps, c4 after 1000); the CPU baseline runs last.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20 (c4: 1000)] [--workload c2] [--no-cpu]
                     [--no-secondary] [--host-overhead]
@@ -315,7 +315,7 @@ def secondary_runs(lib, args):
     import torch
 
     out = {}
-    warmup = max(args.warmup, 20)  # the first calls of a new case page in its pool and tables
+    warmup = max(args.warmup, 100)  # the first calls of a new case page in its pool and tables
     for workload in ("c3", "c5"):
         r = decode_run(lib, workload, args.steps, warmup, args.table_sets, args.seed, 0)
         dc = r.pop("case")
@@ -445,7 +445,11 @@ def main():
     lib = capi.load()
     r = decode_run(lib, args.workload, args.steps, args.warmup, args.table_sets, args.seed, args.partition)
     dc = r["case"]
-
+    # The GPU legs run back to back; the CPU baseline (about a second of host
+    # work with the GPU idle) comes last.
+    secondary = None
+    if args.workload == "c2" and not args.no_secondary:
+        secondary = secondary_runs(lib, args)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(dc, args.cpu_seconds)
@@ -481,10 +485,8 @@ def main():
         "roofline": r["roofline"],
         "cpu_baseline": cpu,
     }
-    if args.workload == "c2" and not args.no_secondary:
-        del dc, r
-        torch.cuda.empty_cache()
-        line["secondary"] = secondary_runs(lib, args)
+    if secondary is not None:
+        line["secondary"] = secondary
     print(json.dumps(line), flush=True)
 
 
