@@ -797,15 +797,47 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill32_kernel(Prefil
 
   // S^T = K . Q^T: group kg's scores in sc[kg]; lane (hf, col) reads token
   // 32 kg + col, logical chunk 2 c + hf.
+#ifndef GK_PREFILL32_AHEAD
+#define GK_PREFILL32_AHEAD 0
+#endif
+  // With GK_PREFILL32_AHEAD = n > 0 the two key groups' chains alternate and
+  // each chunk's K operands are read n chunks ahead, fenced with full
+  // scheduling barriers so the scheduler cannot move the reads back next to
+  // their MFMAs (the wait-count pass then waits only for the older chunk).
   auto scores = [&](const char* kt) __attribute__((always_inline)) {
+    if constexpr (GK_PREFILL32_AHEAD == 0) {
 #pragma unroll
-    for (int kg = 0; kg < 2; ++kg) {
-      sc[kg] = f32x16_t{};
+      for (int kg = 0; kg < 2; ++kg) {
+        sc[kg] = f32x16_t{};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const bf16x8_t kr = *reinterpret_cast<const bf16x8_t*>(kt + (32 * kg + col) * (2 * D) +
+                                                                (((2 * c + hf) ^ swz32(col)) << 4));
+          sc[kg] = mfma32x32(kr, qb[c], sc[kg]);
+        }
+      }
+    } else {
+      constexpr int A = GK_PREFILL32_AHEAD;
+      auto kread = [&](int kg, int c) __attribute__((always_inline)) {
+        return *reinterpret_cast<const bf16x8_t*>(kt + (32 * kg + col) * (2 * D) + (((2 * c + hf) ^ swz32(col)) << 4));
+      };
+      bf16x8_t kr[A + 1][2];
+#pragma unroll
+      for (int c = 0; c < A; ++c) {
+        kr[c][0] = kread(0, c);
+        kr[c][1] = kread(1, c);
+      }
+      sc[0] = sc[1] = f32x16_t{};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const bf16x8_t kr = *reinterpret_cast<const bf16x8_t*>(kt + (32 * kg + col) * (2 * D) +
-                                                              (((2 * c + hf) ^ swz32(col)) << 4));
-        sc[kg] = mfma32x32(kr, qb[c], sc[kg]);
+        if (c + A < NC) {
+          kr[(c + A) % (A + 1)][0] = kread(0, c + A);
+          kr[(c + A) % (A + 1)][1] = kread(1, c + A);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        sc[0] = mfma32x32(kr[c % (A + 1)][0], qb[c], sc[0]);
+        sc[1] = mfma32x32(kr[c % (A + 1)][1], qb[c], sc[1]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
@@ -820,14 +852,32 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill32_kernel(Prefil
     const bf16x4_t v1 = lds_read_tr4(vt + t1 * (2 * D) + ((lc ^ swz32(t1)) << 4) + ((i & 1) << 3));
     return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
   };
+  // P.V; with GK_PREFILL32_AHEAD > 0 the next k chunk's V operands are read
+  // before this chunk's MFMAs, fenced the same way.
   auto accumulate = [&](const char* vt, const bf16x8_t* vfirst) __attribute__((always_inline)) {
+    if constexpr (GK_PREFILL32_AHEAD == 0) {
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc)
+      for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const bf16x8_t v = (kc == 0 && vfirst) ? vfirst[b] : read_v(vt, kc, b);
-        o[b] = mfma32x32(v, pa[kc], o[b]);
+        for (int b = 0; b < NB; ++b) {
+          const bf16x8_t v = (kc == 0 && vfirst) ? vfirst[b] : read_v(vt, kc, b);
+          o[b] = mfma32x32(v, pa[kc], o[b]);
+        }
+    } else {
+      bf16x8_t vv[2][NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) vv[0][b] = vfirst[b];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        if (kc + 1 < KC)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) vv[(kc + 1) & 1][b] = read_v(vt, kc + 1, b);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) o[b] = mfma32x32(vv[kc & 1][b], pa[kc], o[b]);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    }
   };
 
   // Online softmax of the step at tb. Score register r of group kg is key
