@@ -97,6 +97,17 @@ struct PrefillShape {
 //               lane reads its own key's entry with a vector load.
 constexpr int kStepBlocks = 0, kLoadBlocks = 1, kKeyBlocks = 2;
 
+// Head_dim 128 step order. 0: every wave runs Q.K(i), softmax(i), P.V(i)
+// after the step's barrier, so the two waves of a SIMD reach their MFMA and
+// VALU phases together. 1 (build variant): the waves of the second half
+// (waves 4-7, the second wave of each SIMD) run Q.K(i), P.V(i - 1),
+// softmax(i), the same operations on the accumulators in the same order but
+// half a step later, so one wave's softmax can run under the other's MFMAs.
+// V tiles of three steps are then live (three V stages, two K stages).
+#ifndef GK_PREFILL_LAG
+#define GK_PREFILL_LAG 0
+#endif
+
 template <int D, bool SOFTCAP, int MODE>
 __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
   using S = PrefillShape<D>;
@@ -119,8 +130,10 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // pieces for the global stores. Being separate from the stages, a wave
   // starts its output as soon as its own last step ends, with no barrier
   // (132 KiB at head_dim 128, one workgroup per CU either way).
+  constexpr bool kLag = GK_PREFILL_LAG && D >= 128 && !SOFTCAP;  // softcap: no registers to spare
   constexpr int kOutRowBytes = 2 * D + 16;
-  constexpr int kKvBytes = kStages * 2 * S::TILE, kOutBytes = kPrefillWaves * kQrowsPerWave * kOutRowBytes;
+  constexpr int kKvBytes = (kLag ? 5 : kStages * 2) * S::TILE,
+                kOutBytes = kPrefillWaves * kQrowsPerWave * kOutRowBytes;
   __shared__ __attribute__((aligned(16))) char lds[kKvBytes + kOutBytes];
   auto kv = reinterpret_cast<char(*)[2][S::TILE]>(lds);
 
@@ -470,7 +483,68 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   };
 
   static_assert(kStages == 2, "K and V alternate between two stages");
-  if constexpr (!kPingPong) {
+  if constexpr (kLag) {
+    // K stages at lds + s TILE (s = step % 2), V stages after them
+    // (step % 3). One barrier per step, as below: after it every wave's loads
+    // of step i have landed and every wave has finished with K(i - 1) and
+    // V(i - 2), whose stages take step i + 1's loads. The second half's
+    // P.V(i - 1) reads V(i - 1), which stays until the barrier of step i + 1.
+    const bool lead = wave < kPrefillWaves / 2;
+    char* const vstages = lds + 2 * S::TILE;
+    Entries e_next{};
+    {
+      const Offsets first = offsets_of(kb0, entry_of(kb0));
+      issue(first, krs, lds);
+      issue(first, vrs, vstages);
+    }
+    if (1 < nsteps) e_next = entry_of(kb0 + kKeys);
+    int vs = 0;  // V stage of the current step
+    // One loop per half (a single loop with both orders keeps both orders'
+    // registers live); LEAD selects the order at compile time.
+    auto body = [&](int step, auto stage, auto lead_t) __attribute__((always_inline)) {
+      constexpr int cur = decltype(stage)::value, next = cur ^ 1;
+      constexpr bool LEAD = decltype(lead_t)::value;
+      const int tb = kb0 + step * kKeys;
+      const int vnext = vs == 2 ? 0 : vs + 1, vprev = vs == 0 ? 2 : vs - 1;
+      wait_vmem<0>();
+      __syncthreads();
+      wait_vmem_visible();
+      if (step + 1 < nsteps) {
+        const Offsets of = offsets_of(tb + kKeys, e_next);
+        issue(of, krs, lds + next * S::TILE);
+        issue(of, vrs, vstages + vnext * S::TILE);
+        if (step + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
+      }
+      scores(lds + cur * S::TILE);
+      if constexpr (LEAD) {
+        const char* vt = vstages + vs * S::TILE;
+        bf16x8_t vfirst[S::NO];
+#pragma unroll
+        for (int c = 0; c < S::NO; ++c) vfirst[c] = read_v(vt, 0, c);
+        softmax(tb);
+        accumulate(vt, vfirst);
+      } else {
+        if (step > 0) accumulate(vstages + vprev * S::TILE, nullptr);
+        softmax(tb);
+      }
+      vs = vnext;
+    };
+    auto run = [&](auto lead_t) __attribute__((always_inline)) {
+      int step = 0;
+      for (; step + 1 < nsteps; step += 2) {
+        body(step, std::integral_constant<int, 0>{}, lead_t);
+        body(step + 1, std::integral_constant<int, 1>{}, lead_t);
+      }
+      if (step < nsteps) body(step, std::integral_constant<int, 0>{}, lead_t);
+    };
+    if (lead) {
+      run(std::true_type{});
+    } else {
+      run(std::false_type{});
+      // P.V of the last step (its V stage is never refilled).
+      accumulate(vstages + (vs == 0 ? 2 : vs - 1) * S::TILE, nullptr);
+    }
+  } else if constexpr (!kPingPong) {
     // One barrier per step: before it each wave waits for its own loads of
     // the current stage; after it every wave's loads of the stage have landed
     // and every wave has finished the previous step, whose stage is refilled
