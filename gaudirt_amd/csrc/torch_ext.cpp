@@ -719,7 +719,6 @@ class PagedMetadata : public torch::CustomClassHolder {
           tables[r * max_pages + t / page] = mapping_h_[r * context_ + t] / static_cast<int32_t>(page);
     }
     info->block_table_offset = append(tables);
-    while (words.size() % 4) words.push_back(0);
     const int64_t total = host_map || page == 1 ? static_cast<int64_t>(words.size())
                                                 : info->block_table_offset + request_count_ * max_pages;
     info->block_size = page;

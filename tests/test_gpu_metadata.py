@@ -473,6 +473,75 @@ def test_page_aligned_device_metadata(torch_ext, page):
         print(page, orc.check_tolerance(bits(out), ref, MAX_ABS, MEAN_ABS), flush=True)
 
 
+def _irregular_map(rng, requests_n, context, slots, page, kind):
+    """A request map built from `page`-slot blocks, then (kind) left alone,
+    broken in the middle of one page of one request (a continuation elsewhere,
+    aligned only to page / 2), or with one request's blocks shifted by one slot.
+    Every request sees all `context` positions."""
+    # Even block indices only, so a block shifted by one slot never meets another request's block.
+    blocks = 2 * rng.permutation(slots // page // 2 - 2)[: requests_n * context // page] + 2
+    mapping = (blocks.reshape(requests_n, -1)[:, :, None] * page + np.arange(page)).reshape(requests_n, context)
+    r = int(rng.integers(requests_n))
+    if kind == "split" and page >= 2:
+        k = int(rng.integers(context // page))
+        t0 = k * page + page // 2
+        fresh = (slots // page - 1) * page  # the last page's slots, unused by the blocks above
+        mapping[r, t0:(k + 1) * page] = fresh + np.arange(page - page // 2)
+    elif kind == "shift":
+        mapping[r] += 1
+    return mapping.astype(np.int32)
+
+
+@pytest.mark.parametrize("page", [1, 2, 8, 64, 256])
+@pytest.mark.parametrize("kind", ["aligned", "split", "shift"])
+def test_host_page_detection_matches_device(torch_ext, page, kind):
+    """The host constructor finds a map's page size from its breaks in one
+    pass; the checked device constructor finds it from per-page flags (pinned
+    by the oracle). On aligned, mid-page-broken and shifted maps both must pick
+    the same page: their plans (block tables included) and outputs are equal bit
+    for bit."""
+    torch = torch_ext
+    import gaudirt_amd
+
+    rng = np.random.default_rng(page * 7 + len(kind))
+    heads, kv_heads, dim, requests_n, context = 16, 4, 128, 5, 512
+    slots = 64 * 1024
+    scale = float(np.float32(1.0 / math.sqrt(dim)))
+    mapping = _irregular_map(rng, requests_n, context, slots, page, kind)
+    batch_requests = np.arange(requests_n, dtype=np.int64)
+    prefixes, lengths = [context - 1] * requests_n, [1] * requests_n
+    expected = orc.largest_page(orc.page_flags(mapping, batch_requests, prefixes, lengths))
+    if kind == "aligned":
+        assert expected == min(page, 1024)
+    if kind == "split" and page >= 4:
+        assert expected == page // 2
+    if kind == "shift":
+        assert expected == 1
+    positions = np.array(prefixes, dtype=np.int64)
+    locations = mapping[batch_requests, positions].astype(np.int64)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    device_meta = torch.classes.gaudirt.PagedMetadata.from_device(
+        t(locations).cuda(), t(batch_requests).cuda(), t(positions).cuda(), t(mapping).cuda(), prefixes, lengths,
+        slots)
+    host_meta = torch.classes.gaudirt.PagedMetadata(t(locations), t(batch_requests), t(positions), t(mapping), slots)
+    assert torch.equal(device_meta.attention_plan(heads, kv_heads, dim).cpu(),
+                       host_meta.attention_plan(heads, kv_heads, dim).cpu()), (page, kind, expected)
+    gen = torch.Generator().manual_seed(page)
+    q, k, v = (torch.randn(requests_n, w, generator=gen).to(torch.bfloat16).cuda()
+               for w in (heads * dim, kv_heads * dim, kv_heads * dim))
+    outs = []
+    for meta in (device_meta, host_meta):
+        pool = gaudirt_amd.allocate_paged_kv(1, slots, kv_heads, dim)
+        key_pool, value_pool = gaudirt_amd.kv_pool_views(pool, 0)
+        key_pool.copy_(torch.ones(slots, kv_heads, dim, dtype=torch.bfloat16, device="cuda"))
+        value_pool.copy_(torch.arange(slots, device="cuda").to(torch.bfloat16)[:, None, None].expand(slots, kv_heads,
+                                                                                                     dim))
+        outs.append(torch.ops.gaudirt.paged_attn.default(q, k, v, key_pool, value_pool, meta, dim, scale))
+        torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (page, kind)
+    assert torch.isfinite(outs[0].float()).all()
+
+
 # ---------------------------------------------------------------------------
 # _C._allocate_paged_slots / _C._release_paged_slots
 # ---------------------------------------------------------------------------
