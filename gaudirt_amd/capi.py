@@ -21,6 +21,7 @@ GK_ERR_HIP = 3
 GK_ERR_OUT_OF_MEMORY = 4
 GK_ERR_WORKSPACE = 5
 GK_DECODE_SCRATCH_BYTES = 32 << 20
+GK_METADATA_INLINE_WORDS = 768
 
 # Every function include/gaudirt_amd.h declares.
 EXPORTED = [
@@ -107,6 +108,7 @@ class MetadataParams(_Sized):
         ("slots", c_i64),
         ("out_locations", c_void_p), ("out_requests", c_void_p), ("out_positions", c_void_p),
         ("out_tokens", c_void_p), ("status", c_void_p), ("token_status", c_void_p), ("page_flags", c_void_p),
+        ("staged_words", c_void_p), ("staged_device", c_void_p), ("staged_count", c_i32),
     ]
 
 

@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstring>
 
 namespace gk {
 namespace {
@@ -81,10 +82,54 @@ __global__ __launch_bounds__(kThreads) void fill_kernel(int32_t* p, int64_t n, i
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) p[i] = v;
 }
 
+// Host-staged words carried in the launch's own kernel arguments: the
+// kernel stores them at `device`, and inputs that point into that range are
+// read from the argument copy (the grid is writing the memory they name).
+template <bool kStaged>
+struct Staged {};
+template <>
+struct Staged<true> {
+  int32_t* device;
+  int32_t count;
+  int32_t row_seq, seq_prefix, seq_first_row, positions;  // word offsets into `words`, or -1
+  int32_t words[GK_METADATA_INLINE_WORDS];
+};
+
+template <bool kStaged>
+__device__ __forceinline__ int32_t staged_word(const Staged<kStaged>& s, int off, const int32_t* p, int64_t i) {
+  if constexpr (kStaged) {
+    if (off >= 0) return s.words[off + i];
+  }
+  return p[i];
+}
+
+template <bool kStaged>
+__device__ __forceinline__ int64_t staged_index(const Staged<kStaged>& s, int off, const void* p, int is64,
+                                                int64_t i) {
+  if constexpr (kStaged) {
+    if (off >= 0) {
+      if (!is64) return s.words[off + i];
+      const uint32_t lo = static_cast<uint32_t>(s.words[off + 2 * i]);
+      return static_cast<int64_t>(static_cast<uint64_t>(static_cast<uint32_t>(s.words[off + 2 * i + 1])) << 32 | lo);
+    }
+  }
+  return load_index(p, is64, i);
+}
+
 // Pass 1, one thread per padded row: int32 rows (zeros past `rows`), range
 // codes 1/2, mapping agreement 3, expected position 5, token range; rows with
 // no code claim their output slot in the hash table.
-__global__ __launch_bounds__(kThreads) void normalize_rows_kernel(NormArgs a) {
+template <bool kStaged>
+__global__ __launch_bounds__(kThreads) void normalize_rows_kernel(NormArgs a, Staged<kStaged> st) {
+  int row_seq_off = -1, prefix_off = -1, first_off = -1, positions_off = -1;
+  if constexpr (kStaged) {
+    for (int j = blockIdx.x * kThreads + threadIdx.x; j < st.count; j += gridDim.x * kThreads)
+      st.device[j] = st.words[j];
+    row_seq_off = st.row_seq;
+    prefix_off = st.seq_prefix;
+    first_off = st.seq_first_row;
+    positions_off = st.positions;
+  }
   for (int i = blockIdx.x * kThreads + threadIdx.x; i < a.padded_rows; i += gridDim.x * kThreads) {
     if (i >= a.rows) {
       a.out_locations[i] = 0;
@@ -95,9 +140,9 @@ __global__ __launch_bounds__(kThreads) void normalize_rows_kernel(NormArgs a) {
       if (a.token_status) a.token_status[i] = 0;
       continue;
     }
-    const int seq = a.row_seq[i];
+    const int seq = staged_word(st, row_seq_off, a.row_seq, i);
     const int64_t loc = load_index(a.locations, a.loc64, i);
-    const int64_t pos = load_index(a.positions, a.pos64, i);
+    const int64_t pos = staged_index(st, positions_off, a.positions, a.pos64, i);
     const int64_t req = load_index(a.batch_requests, a.req64, seq);
     a.out_locations[i] = static_cast<int32_t>(loc);
     a.out_positions[i] = static_cast<int32_t>(pos);
@@ -113,7 +158,9 @@ __global__ __launch_bounds__(kThreads) void normalize_rows_kernel(NormArgs a) {
     else if (req < 0 || req >= a.requests) code = 2;
     if (a.mapping) {
       if (code == 0 && a.mapping[req * a.context + pos] != static_cast<int32_t>(loc)) code = 3;
-      if (code == 0 && pos != (int64_t)a.seq_prefix[seq] + (i - a.seq_first_row[seq])) code = 5;
+      if (code == 0 && pos != (int64_t)staged_word(st, prefix_off, a.seq_prefix, seq) +
+                                   (i - staged_word(st, first_off, a.seq_first_row, seq)))
+        code = 5;
       if (code == 0) {
         const int32_t key = static_cast<int32_t>(loc);
         uint32_t h = slot_hash(key, a.table_mask);
@@ -320,6 +367,45 @@ extern "C" int gk_metadata_normalize(const gk_metadata_params* p, void* workspac
       (p->token_ids && !p->out_tokens) || (p->page_flags && !p->mapping) ||
       ((checks || p->page_flags) && p->visible_total > 0 && !p->seq_visible))
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_metadata_normalize: null pointer");
+  // Staged words: where each input that points into them starts, as a word
+  // offset; an input only partly inside, or an input the kernel does not
+  // redirect (or an output) inside, is refused.
+  gk::Staged<true> st{};
+  if (p->staged_words || p->staged_device || p->staged_count) {
+    if (!p->staged_words || !p->staged_device || p->staged_count <= 0 ||
+        p->staged_count > GK_METADATA_INLINE_WORDS)
+      return fail(GK_ERR_INVALID_ARGUMENT, "gk_metadata_normalize: staged words need a host pointer, a device "
+                                           "pointer and 1 to " + std::to_string(GK_METADATA_INLINE_WORDS) + " words");
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p->staged_device);
+    const uintptr_t hi = lo + static_cast<uintptr_t>(p->staged_count) * sizeof(int32_t);
+    const auto inside = [&](const void* q) {
+      const uintptr_t a = reinterpret_cast<uintptr_t>(q);
+      return q && a >= lo && a < hi;
+    };
+    bool bad = false;
+    const auto offset = [&](const void* q, int64_t words) -> int32_t {
+      if (!inside(q)) return -1;
+      const uintptr_t a = reinterpret_cast<uintptr_t>(q);
+      if ((a - lo) % sizeof(int32_t) || a + static_cast<uintptr_t>(words) * sizeof(int32_t) > hi) bad = true;
+      return static_cast<int32_t>((a - lo) / sizeof(int32_t));
+    };
+    st.device = p->staged_device;
+    st.count = p->staged_count;
+    st.row_seq = offset(p->row_seq, p->rows);
+    st.seq_prefix = offset(p->seq_prefix, p->batch);
+    st.seq_first_row = offset(p->seq_first_row, p->batch);
+    st.positions = offset(p->positions, static_cast<int64_t>(p->rows) * (p->positions_int64 ? 2 : 1));
+    for (const void* q : {p->locations, p->batch_requests, p->token_ids, static_cast<const void*>(p->mapping),
+                          static_cast<const void*>(p->out_locations), static_cast<const void*>(p->out_requests),
+                          static_cast<const void*>(p->out_positions), static_cast<const void*>(p->out_tokens),
+                          static_cast<const void*>(p->status), static_cast<const void*>(p->token_status),
+                          static_cast<const void*>(p->page_flags)})
+      bad = bad || inside(q);
+    if (bad)
+      return fail(GK_ERR_INVALID_ARGUMENT,
+                  "gk_metadata_normalize: an input or output overlaps the staged words in an unsupported way");
+    std::memcpy(st.words, p->staged_words, static_cast<size_t>(p->staged_count) * sizeof(int32_t));
+  }
   const size_t need = checks ? gk_metadata_workspace_bytes(p->rows, p->batch) : 0;
   if (checks && (workspace_bytes < need || !workspace))
     return fail(GK_ERR_WORKSPACE, "gk_metadata_normalize: workspace too small (" + std::to_string(need) + " bytes)");
@@ -363,7 +449,10 @@ extern "C" int gk_metadata_normalize(const gk_metadata_params* p, void* workspac
     gk::fill_kernel<<<gk::grid_for(p->batch), gk::kThreads, 0, stream>>>(a.seq_bits, p->batch, 0);
   }
   if (p->page_flags) gk::fill_kernel<<<1, gk::kThreads, 0, stream>>>(p->page_flags, 1, 0);
-  gk::normalize_rows_kernel<<<gk::grid_for(p->padded_rows), gk::kThreads, 0, stream>>>(a);
+  if (st.count)
+    gk::normalize_rows_kernel<true><<<gk::grid_for(p->padded_rows), gk::kThreads, 0, stream>>>(a, st);
+  else
+    gk::normalize_rows_kernel<false><<<gk::grid_for(p->padded_rows), gk::kThreads, 0, stream>>>(a, {});
   if ((checks || p->page_flags) && p->visible_total > 0) {
     gk::NormArgs b = a;
     b.mapping = p->mapping;

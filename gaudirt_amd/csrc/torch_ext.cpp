@@ -479,7 +479,10 @@ class PagedMetadata : public torch::CustomClassHolder {
     std::copy(seq_first.begin(), seq_first.end(), host.begin() + first_offset);
     std::memcpy(host.data() + visible_offset, seq_visible.data(), batch * sizeof(int64_t));
     if (positions_on_cpu) std::memcpy(host.data() + model_offset, positions.data_ptr<int64_t>(), m * sizeof(int64_t));
-    storage_ = upload_words(host, words);
+    // Up to GK_METADATA_INLINE_WORDS staged words travel in the normalisation
+    // launch's arguments (no upload); more go through pinned staging.
+    const bool inline_staged = staged_words <= GK_METADATA_INLINE_WORDS;
+    storage_ = inline_staged ? at::empty({words}, device_int32()) : upload_words(host, words);
     int32_t* base = storage_.data_ptr<int32_t>();
     header_ = storage_.narrow(0, header_offset, 1);
     last_token_indices_ = storage_.narrow(0, last_offset, batch);
@@ -530,6 +533,11 @@ class PagedMetadata : public torch::CustomClassHolder {
     p.out_requests = base + requests_offset;
     p.out_positions = base + positions_offset;
     p.out_tokens = has_tokens ? base + tokens_offset : nullptr;
+    if (inline_staged) {
+      p.staged_words = host.data();
+      p.staged_device = base;
+      p.staged_count = static_cast<int32_t>(staged_words);
+    }
     at::Tensor workspace;
     if (!scheduler_owned) {
       p.mapping = mapping.data_ptr<int32_t>();

@@ -285,7 +285,18 @@ int gk_rotary_kv_store(const gk_rotary_params* params, hipStream_t stream);
  * checked (scheduler-owned inputs) and no workspace is needed.
  * seq_visible[s] = sum over earlier sequences of (prefix + length);
  * visible_total = the sum over all.
+ *
+ * Staged words (optional, this library's own addition): staged_count <=
+ * GK_METADATA_INLINE_WORDS host int32 words that the launch itself stores at
+ * staged_device[0 .. staged_count), carried in the kernel's arguments, so a
+ * caller that builds its row_seq / seq_prefix / seq_first_row / seq_visible
+ * words on the host needs no separate upload (and its dependency wait) and
+ * may reuse the host buffer once the call returns. row_seq, seq_prefix,
+ * seq_first_row, positions and seq_visible may point into that range (they
+ * are then read as staged); every other input and output must lie outside it.
  * ------------------------------------------------------------------------- */
+#define GK_METADATA_INLINE_WORDS 768
+
 typedef struct gk_metadata_params {
   size_t struct_size;           /* sizeof(gk_metadata_params) as the caller was built; checked */
   const void* locations;        /* [rows] int32 or int64 (locations_int64) */
@@ -308,6 +319,9 @@ typedef struct gk_metadata_params {
   int32_t* status;              /* [padded_rows] or NULL */
   int32_t* token_status;        /* [padded_rows] 1 = token outside [0, vocabulary), or NULL */
   int32_t* page_flags;          /* [1] or NULL */
+  const int32_t* staged_words;  /* [staged_count] host words, or NULL */
+  int32_t* staged_device;       /* device destination of the staged words, or NULL */
+  int32_t staged_count;         /* 0, or 1 .. GK_METADATA_INLINE_WORDS */
 } gk_metadata_params;
 
 size_t gk_metadata_workspace_bytes(int32_t rows, int32_t batch);

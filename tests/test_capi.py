@@ -132,6 +132,44 @@ def test_metadata_and_allocator_validation(lib):
     assert rc == capi.GK_ERR_WORKSPACE
 
 
+def test_metadata_staged_words_validation(lib):
+    """Staged-word arguments are refused before any launch: missing pointers,
+    more than GK_METADATA_INLINE_WORDS words, an input only partly inside the
+    staged range, an unredirected input or an output inside it."""
+    header = (ROOT / "include" / "gaudirt_amd.h").read_text()
+    assert f"#define GK_METADATA_INLINE_WORDS {capi.GK_METADATA_INLINE_WORDS}" in header
+    host = (ctypes.c_int32 * capi.GK_METADATA_INLINE_WORDS)()
+    staged = 1 << 40  # device addresses are never dereferenced on the host
+    p = capi.MetadataParams()
+    p.rows, p.padded_rows, p.batch, p.requests, p.context, p.slots = 4, 4, 2, 2, 64, 128
+    names = ("locations", "batch_requests", "positions", "row_seq", "seq_prefix", "seq_first_row",
+             "out_locations", "out_requests", "out_positions")
+    for i, name in enumerate(names):
+        setattr(p, name, (1 << 36) + 4096 * i)
+
+    def refused(match):
+        assert lib.gk_metadata_normalize(ctypes.byref(p), None, 0, None) == capi.GK_ERR_INVALID_ARGUMENT
+        assert match in lib.gk_last_error().decode()
+
+    p.staged_words, p.staged_device, p.staged_count = ctypes.addressof(host), staged, 0
+    refused("staged words need")
+    p.staged_count = capi.GK_METADATA_INLINE_WORDS + 1
+    refused("staged words need")
+    p.staged_count, p.staged_words = 64, None
+    refused("staged words need")
+    p.staged_words = ctypes.addressof(host)
+    p.row_seq = staged + 4 * 62  # 4 rows from word 62 of 64
+    refused("overlaps the staged words")
+    p.row_seq = staged + 2  # not word aligned
+    refused("overlaps the staged words")
+    p.row_seq = staged
+    p.locations = staged + 64
+    refused("overlaps the staged words")
+    p.locations = 1 << 36
+    p.out_positions = staged + 4 * 63
+    refused("overlaps the staged words")
+
+
 def test_rotary_validation(lib):
     p = capi.RotaryParams()
     p.struct_size = 24

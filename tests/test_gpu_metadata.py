@@ -75,7 +75,11 @@ def prepare(torch, locations, requests, positions, mapping, prefixes, lengths, s
 # ---------------------------------------------------------------------------
 
 def normalize(torch, locations, batch_requests, positions, mapping, prefixes, lengths, slots, tokens=None,
-              vocabulary=0, validate=True):
+              vocabulary=0, validate=True, staged=False):
+    """Runs gk_metadata_normalize. With `staged`, row_seq, seq_prefix,
+    seq_first_row, seq_visible (and positions, where they fit) are passed as
+    staged words: the launch stores them itself into a device buffer that the
+    input pointers name, and result["staged"] holds that buffer afterwards."""
     from gaudirt_amd import capi
 
     lib = capi.load()
@@ -114,6 +118,26 @@ def normalize(torch, locations, batch_requests, positions, mapping, prefixes, le
     if validate:
         p.status = out["status"].data_ptr()
         p.page_flags = flags.data_ptr()
+    if staged:
+        sections = [("row_seq", row_seq), ("prefix", np.array(prefixes, dtype=np.int32)), ("first", first),
+                    ("visible", seq_visible)]
+        if np.asarray(positions).nbytes // 4 + sum(a.nbytes // 4 for _, a in sections) <= capi.GK_METADATA_INLINE_WORDS:
+            sections.append(("pos", np.ascontiguousarray(positions)))
+        host = np.concatenate([a.view(np.int32) for _, a in sections]).astype(np.int32)
+        assert host.size <= capi.GK_METADATA_INLINE_WORDS
+        staged_dev = torch.full((host.size,), -9, dtype=torch.int32, device="cuda")
+        offset = 0
+        for name, a in sections:
+            pointer = staged_dev.data_ptr() + 4 * offset
+            if name == "pos":
+                p.positions = pointer
+            else:
+                setattr(p, {"row_seq": "row_seq", "prefix": "seq_prefix", "first": "seq_first_row",
+                            "visible": "seq_visible"}[name], pointer)
+            offset += a.nbytes // 4
+        p.staged_words = host.ctypes.data
+        p.staged_device = staged_dev.data_ptr()
+        p.staged_count = host.size
     need = lib.gk_metadata_workspace_bytes(rows, batch)
     ws = torch.empty(need, dtype=torch.uint8, device="cuda")
     capi.check(lib.gk_metadata_normalize(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), need,
@@ -121,16 +145,20 @@ def normalize(torch, locations, batch_requests, positions, mapping, prefixes, le
     torch.cuda.synchronize()
     result = {n: t.cpu().numpy() for n, t in out.items()}
     result["flags"] = int(flags.item())
+    if staged:
+        result["staged"] = staged_dev.cpu().numpy()
+        assert np.array_equal(result["staged"], host)
+        result["staged_positions"] = sections[-1][0] == "pos"
     return result
 
 
-def random_problem(rng, kind, requests_n=16, context=512, slots=9000, page=None):
+def random_problem(rng, kind, requests_n=16, context=512, slots=9000, page=None, max_batch=12):
     if page:
         blocks = rng.permutation(slots // page)[: requests_n * context // page]
         mapping = (blocks[:, None] * page + np.arange(page)).reshape(requests_n, context).astype(np.int32)
     else:
         mapping = rng.permutation(slots)[: requests_n * context].reshape(requests_n, context).astype(np.int32)
-    batch = int(rng.integers(1, 12))
+    batch = int(rng.integers(1, max_batch))
     batch_requests = rng.permutation(requests_n)[:batch].astype(np.int64)
     prefixes = [int(x) for x in rng.integers(0, 300, batch)]
     lengths = [int(x) for x in rng.integers(1, 40, batch)]
@@ -179,6 +207,38 @@ def test_status_codes_match_oracle(torch_ext, kind):
         assert np.array_equal(got["req"][:rows], np.repeat(req, lengths).astype(np.int32))
         for name in ("loc", "req", "pos"):
             assert (got[name][rows:] == 0).all()
+
+
+@pytest.mark.parametrize("kind", range(8))
+def test_staged_words_match_device_inputs(torch_ext, kind):
+    """Staged words carried in the launch (row_seq, seq_prefix, seq_first_row,
+    seq_visible and, where they fit, positions) give the same codes, flags and
+    rows as the same words read from device memory, and land in the device
+    buffer their pointers name."""
+    torch = torch_ext
+    rng = np.random.default_rng(900 + kind)
+    redirected = 0
+    for trial in range(4):
+        page = [None, 16][trial % 2]
+        loc, req, pos, mapping, prefixes, lengths, slots = random_problem(rng, kind, page=page,
+                                                                          max_batch=[12, 3][trial % 2])
+        if trial >= 2:
+            loc, pos = loc.astype(np.int32) if np.abs(loc).max() < 2**31 else loc, pos.astype(np.int32)
+        tokens = rng.integers(0, 32000, len(loc)).astype(np.int64)
+        plain = normalize(torch, loc, req, pos, mapping, prefixes, lengths, slots, tokens=tokens, vocabulary=32000)
+        staged = normalize(torch, loc, req, pos, mapping, prefixes, lengths, slots, tokens=tokens,
+                           vocabulary=32000, staged=True)
+        print("kind", kind, "trial", trial, "rows", len(loc), "positions staged", staged["staged_positions"],
+              flush=True)
+        redirected += staged["staged_positions"]
+        for name in ("loc", "req", "pos", "tok", "status", "token_status", "flags"):
+            assert np.array_equal(plain[name], staged[name]), name
+        want = orc.metadata_codes(loc, req, pos, mapping, prefixes, lengths, slots)
+        assert list(staged["status"][:len(loc)]) == want
+        unchecked = normalize(torch, loc, req, pos, mapping, prefixes, lengths, slots, validate=False, staged=True)
+        for name in ("loc", "req", "pos"):
+            assert np.array_equal(plain[name], unchecked[name]), name
+    assert redirected > 0
 
 
 def test_tokens_and_unchecked_normalisation(torch_ext):
