@@ -32,6 +32,7 @@
 #include <mutex>
 #include <numeric>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "gaudirt_amd.h"
@@ -68,15 +69,41 @@ at::TensorOptions device_int32() {
 // words.size() filled) on the current stream through pinned staging: the
 // host does not wait for queued device work, and torch's host allocator
 // keeps the staging block until the copy has run.
-at::Tensor upload_words(const std::vector<int32_t>& words, int64_t total) {
+at::Tensor upload_words(const int32_t* words, int64_t count, int64_t total) {
   auto device = at::empty({total}, device_int32());
-  if (!words.empty()) {
-    auto host = at::empty({static_cast<int64_t>(words.size())}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
-    std::memcpy(host.data_ptr<int32_t>(), words.data(), words.size() * sizeof(int32_t));
-    device.narrow(0, 0, static_cast<int64_t>(words.size())).copy_(host, /*non_blocking=*/true);
+  if (count > 0) {
+    auto host = at::empty({count}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
+    std::memcpy(host.data_ptr<int32_t>(), words, count * sizeof(int32_t));
+    device.narrow(0, 0, count).copy_(host, /*non_blocking=*/true);
   }
   return device;
 }
+at::Tensor upload_words(const std::vector<int32_t>& words, int64_t total) {
+  return upload_words(words.data(), static_cast<int64_t>(words.size()), total);
+}
+
+// Allocator whose resize leaves new elements uninitialised, for host copies
+// that are written in full right after (zero-filling a 1 MB request map first
+// cost about as much as copying it).
+template <class T>
+struct UninitAllocator : std::allocator<T> {
+  template <class U>
+  struct rebind {
+    using other = UninitAllocator<U>;
+  };
+  UninitAllocator() = default;
+  template <class U>
+  UninitAllocator(const UninitAllocator<U>&) noexcept {}
+  template <class U>
+  void construct(U* p) noexcept {
+    ::new (static_cast<void*>(p)) U;
+  }
+  template <class U, class... A>
+  void construct(U* p, A&&... a) {
+    ::new (static_cast<void*>(p)) U(std::forward<A>(a)...);
+  }
+};
+using HostWords = std::vector<int32_t, UninitAllocator<int32_t>>;
 
 // Word offset of the next 256-byte aligned section of a packed int32 buffer.
 int64_t reserve_words(int64_t& cursor, int64_t count) {
@@ -260,31 +287,18 @@ class PagedMetadata : public torch::CustomClassHolder {
                     context <= std::numeric_limits<int32_t>::max() &&
                     mapping.numel() <= std::numeric_limits<int32_t>::max(),
                 "GaudiRT: paged metadata dimensions outside supported range");
-    // Whole-tensor checks first, then one failure code per row; the first
-    // failing row reports its first failing check, so the messages and their
-    // order are those of the reference's row-by-row scan. The request map is
-    // range-checked in one pass while it is copied to the host vector.
+    // The reference checks the whole request map first, then each row (the
+    // first failing row reports its first failing check), then every visible
+    // prefix in (request, position) order; the first failure of that order is
+    // the one reported. Here the row checks read the map from the caller's
+    // tensor, and one pass per request row copies and range-checks the row
+    // and, while it is in cache, walks the request's visible prefix; faults
+    // are recorded and raised in the reference's order after the pass.
     const int64_t map_n = mapping.numel();
-    mapping_h_.resize(map_n);
-    bool map_in_range = true;
-    if (mapping.scalar_type() == at::kInt) {
-      const int32_t* src = mapping.data_ptr<int32_t>();
-      int32_t lo = 0, hi = 0;
-      if (map_n) lo = hi = src[0];
-      for (int64_t i = 0; i < map_n; ++i) {
-        lo = std::min(lo, src[i]);
-        hi = std::max(hi, src[i]);
-      }
-      map_in_range = lo >= -1 && hi < slots;
-      if (map_in_range) std::memcpy(mapping_h_.data(), src, map_n * sizeof(int32_t));
-    } else {
-      const int64_t* src = mapping.data_ptr<int64_t>();
-      for (int64_t i = 0; i < map_n && map_in_range; ++i) {
-        map_in_range = src[i] >= -1 && src[i] < slots;
-        mapping_h_[i] = static_cast<int32_t>(src[i]);
-      }
-    }
-    TORCH_CHECK(map_in_range, "GaudiRT: request-to-token slot is out of range");
+    const bool map32 = mapping.scalar_type() == at::kInt;
+    const auto map_at = [&](int64_t i) -> int64_t {
+      return map32 ? mapping.data_ptr<int32_t>()[i] : mapping.data_ptr<int64_t>()[i];
+    };
     const auto loc = locations.to(at::kLong), req = requests.to(at::kLong), pos = positions.to(at::kLong);
     const int64_t* loc_p = loc.data_ptr<int64_t>();
     const int64_t* req_p = req.data_ptr<int64_t>();
@@ -295,26 +309,124 @@ class PagedMetadata : public torch::CustomClassHolder {
       if (loc_p[i] < 0 || loc_p[i] >= slots || req_p[i] < 0 || req_p[i] >= request_count || pos_p[i] < 0 ||
           pos_p[i] >= context)
         fault[i] = kRowRange;
-      else if (mapping_h_[req_p[i] * context + pos_p[i]] != loc_p[i])
+      else if (map_at(req_p[i] * context + pos_p[i]) != loc_p[i])
         fault[i] = kRowMismatch;
     }
     // Output slots sorted with their row: a slot's rows after its first are
-    // duplicates, and the sorted list answers "which row writes slot s" below.
+    // duplicates, and the sorted list answers "which rows write slots in
+    // [a, b)" below.
     std::vector<int64_t> by_slot(m);
     std::iota(by_slot.begin(), by_slot.end(), int64_t{0});
     std::sort(by_slot.begin(), by_slot.end(),
               [&](int64_t a, int64_t b) { return loc_p[a] != loc_p[b] ? loc_p[a] < loc_p[b] : a < b; });
     for (int64_t k = 1; k < m; ++k)
       if (loc_p[by_slot[k]] == loc_p[by_slot[k - 1]] && fault[by_slot[k]] == kRowOk) fault[by_slot[k]] = kRowDuplicate;
-    const auto bad = std::find_if(fault.begin(), fault.end(), [](int f) { return f != kRowOk; });
-    if (bad != fault.end()) {
-      TORCH_CHECK(*bad != kRowRange, "GaudiRT: paged metadata index is out of range");
-      TORCH_CHECK(*bad != kRowMismatch, "GaudiRT: output slot does not match request-to-token mapping");
+    const auto bad_row = std::find_if(fault.begin(), fault.end(), [](int f) { return f != kRowOk; });
+    const bool rows_ok = bad_row == fault.end();
+    if (rows_ok) {
+      locations_h_.assign(loc_p, loc_p + m);
+      requests_h_.assign(req_p, req_p + m);
+      positions_h_.assign(pos_p, pos_p + m);
+      max_position_.assign(request_count, -1);
+      for (int64_t i = 0; i < m; ++i)
+        max_position_[requests_h_[i]] = std::max(max_position_[requests_h_[i]], positions_h_[i]);
+    }
+    // Every request's visible prefix (positions up to its last row) must have
+    // slots, none of them the output slot of another (request, position). The
+    // prefix is walked as runs of consecutive slots (slot - position constant,
+    // compared eight positions at a time); a run's slot range is looked up
+    // among the written slots only when a 2^16-bit filter of them (slot mod
+    // 2^16) has a bit in it. The same walk finds the page size of the map: the
+    // largest power of two P <= 1024 such that each visible token t sits at
+    // map[t - t % P] + t % P with map[t - t % P] a multiple of P. That holds
+    // exactly when every run start (t = 0, or map[t] != map[t - 1] + 1) has
+    // both t and map[t] divisible by P, so P is the lowest set bit of the OR
+    // of those values.
+    std::vector<uint64_t> written(1024, 0);
+    for (int64_t i = 0; i < m; ++i) written[(loc_p[i] >> 6) & 1023] |= uint64_t{1} << (loc_p[i] & 63);
+    const auto filter_hit = [&](int32_t first_slot, int64_t count) {
+      uint32_t bit = static_cast<uint32_t>(first_slot) & 65535u;
+      int64_t left = std::min<int64_t>(count, 65536);
+      while (left > 0) {
+        const uint32_t off = bit & 63u;
+        const int64_t take = std::min<int64_t>(left, 64 - off);
+        const uint64_t mask = (take == 64 ? ~uint64_t{0} : (uint64_t{1} << take) - 1) << off;
+        if (written[bit >> 6] & mask) return true;
+        left -= take;
+        bit = (bit + static_cast<uint32_t>(take)) & 65535u;
+      }
+      return false;
+    };
+    enum PrefixFault : int { kPrefixOk = 0, kPrefixMissing, kPrefixAlias };
+    int prefix_fault = kPrefixOk;
+    uint32_t breaks = 0;
+    const auto walk_prefix = [&](int64_t request) {
+      const int32_t* row_map = mapping_h_.data() + request * context;
+      const int32_t last = max_position_[request];
+      int32_t p = 0;
+      while (p <= last) {
+        const int32_t s0 = row_map[p];
+        if (s0 < 0) {
+          prefix_fault = kPrefixMissing;
+          return;
+        }
+        breaks |= static_cast<uint32_t>(p) | static_cast<uint32_t>(s0);
+        const int32_t shift = s0 - p;  // slot - position along the run (slots are below 2^31 - 1)
+        int32_t q = p + 1;
+        while (q + 8 <= last + 1) {
+          bool broken = false;
+          for (int k = 0; k < 8; ++k) broken |= row_map[q + k] - (q + k) != shift;
+          if (broken) break;
+          q += 8;
+        }
+        while (q <= last && row_map[q] - q == shift) ++q;
+        // Positions [p, q) hold slots [s0, s0 + q - p); their writers, in slot
+        // (and so position) order, must be this request at that position.
+        if (filter_hit(s0, q - p)) {
+          auto it = std::lower_bound(by_slot.begin(), by_slot.end(), s0,
+                                     [&](int64_t row, int32_t s) { return loc_p[row] < s; });
+          for (; it != by_slot.end() && loc_p[*it] < static_cast<int64_t>(s0) + (q - p); ++it) {
+            const int64_t position = p + (loc_p[*it] - s0);
+            if (requests_h_[*it] != request || positions_h_[*it] != position) {
+              prefix_fault = kPrefixAlias;
+              return;
+            }
+          }
+        }
+        p = q;
+      }
+    };
+    mapping_h_.resize(map_n);
+    const uint32_t slot_limit = static_cast<uint32_t>(slots);
+    uint32_t out_of_range = 0;
+    for (int64_t request = 0; request < request_count; ++request) {
+      int32_t* dst = mapping_h_.data() + request * context;
+      if (map32) {
+        // -1 <= slot < slots as one unsigned comparison (slots <= INT32_MAX).
+        const int32_t* src = mapping.data_ptr<int32_t>() + request * context;
+        for (int64_t t = 0; t < context; ++t) {
+          const int32_t slot = src[t];
+          dst[t] = slot;
+          out_of_range |= static_cast<uint32_t>(static_cast<uint32_t>(slot) + 1u > slot_limit);
+        }
+      } else {
+        const int64_t* src = mapping.data_ptr<int64_t>() + request * context;
+        for (int64_t t = 0; t < context; ++t) {
+          const int64_t slot = src[t];
+          dst[t] = static_cast<int32_t>(slot);
+          out_of_range |= static_cast<uint32_t>(slot < -1 || slot >= slots);
+        }
+      }
+      if (rows_ok && !out_of_range && prefix_fault == kPrefixOk && max_position_[request] >= 0) walk_prefix(request);
+    }
+    TORCH_CHECK(!out_of_range, "GaudiRT: request-to-token slot is out of range");
+    if (!rows_ok) {
+      TORCH_CHECK(*bad_row != kRowRange, "GaudiRT: paged metadata index is out of range");
+      TORCH_CHECK(*bad_row != kRowMismatch, "GaudiRT: output slot does not match request-to-token mapping");
       TORCH_CHECK(false, "GaudiRT: duplicate output KV slot");
     }
-    locations_h_.assign(loc_p, loc_p + m);
-    requests_h_.assign(req_p, req_p + m);
-    positions_h_.assign(pos_p, pos_p + m);
+    TORCH_CHECK(prefix_fault != kPrefixMissing, "GaudiRT: missing KV slot in a visible prefix");
+    TORCH_CHECK(prefix_fault != kPrefixAlias, "GaudiRT: output KV slot aliases another visible prefix position");
     // Runs of consecutive positions of one request, from their boundaries.
     std::vector<int32_t> run_starts;
     for (int64_t i = 0; i < m; ++i)
@@ -323,40 +435,6 @@ class PagedMetadata : public torch::CustomClassHolder {
     run_starts.push_back(static_cast<int32_t>(m));
     for (size_t k = 0; k + 1 < run_starts.size(); ++k)
       sequences_.push_back({run_starts[k], run_starts[k + 1] - run_starts[k], positions_h_[run_starts[k]]});
-    // Every request's visible prefix (positions up to its last row) must have
-    // slots, none of them the output slot of another (request, position). The
-    // written slots also go into a 2^16-bit filter (slot mod 2^16), so the scan
-    // looks a slot up among them only when its filter bit is set.
-    max_position_.assign(request_count, -1);
-    for (int64_t i = 0; i < m; ++i)
-      max_position_[requests_h_[i]] = std::max(max_position_[requests_h_[i]], positions_h_[i]);
-    std::vector<uint64_t> written(1024, 0);
-    for (int64_t i = 0; i < m; ++i) written[(loc_p[i] >> 6) & 1023] |= uint64_t{1} << (loc_p[i] & 63);
-    const auto writer_of = [&](int32_t slot) -> int64_t {  // the row writing `slot`, or -1
-      const auto it = std::lower_bound(by_slot.begin(), by_slot.end(), slot,
-                                       [&](int64_t row, int32_t s) { return loc_p[row] < s; });
-      return it != by_slot.end() && loc_p[*it] == slot ? *it : -1;
-    };
-    // The same scan finds the page size of the map: the largest power of two
-    // P <= 1024 such that each visible token t sits at map[t - t % P] + t % P
-    // with map[t - t % P] a multiple of P. That holds exactly when every break
-    // of the map (t = 0, or map[t] != map[t - 1] + 1) has both t and map[t]
-    // divisible by P, so P is the lowest set bit of the OR of those values.
-    uint32_t breaks = 0;
-    for (int64_t request = 0; request < request_count; ++request) {
-      const int32_t* row_map = mapping_h_.data() + request * context;
-      for (int32_t position = 0; position <= max_position_[request]; ++position) {
-        const int32_t slot = row_map[position];
-        TORCH_CHECK(slot >= 0, "GaudiRT: missing KV slot in a visible prefix");
-        if (position == 0 || slot != row_map[position - 1] + 1)
-          breaks |= static_cast<uint32_t>(position) | static_cast<uint32_t>(slot);
-        if (written[(slot >> 6) & 1023] & (uint64_t{1} << (slot & 63))) {
-          const int64_t writer = writer_of(slot);
-          TORCH_CHECK(writer < 0 || (requests_h_[writer] == request && positions_h_[writer] == position),
-                      "GaudiRT: output KV slot aliases another visible prefix position");
-        }
-      }
-    }
     page_ = 1024;
     while (page_ > 1 && (breaks & static_cast<uint32_t>(page_ - 1))) page_ >>= 1;
     rows_ = m;
@@ -764,13 +842,16 @@ class PagedMetadata : public torch::CustomClassHolder {
   // The request map on the device: the device constructors' own input, or
   // (host constructor) the host copy, uploaded on the current stream on first use.
   const at::Tensor& device_mapping() {
-    if (!mapping_.defined()) mapping_ = upload_words(mapping_h_, request_count_ * context_).view({request_count_, context_});
+    if (!mapping_.defined())
+      mapping_ = upload_words(mapping_h_.data(), static_cast<int64_t>(mapping_h_.size()), request_count_ * context_)
+                     .view({request_count_, context_});
     return mapping_;
   }
 
   int64_t rows_ = 0, slots_ = 0, request_count_ = 0, context_ = 0, vocabulary_ = 0, page_ = 1;
   // Host copies (host constructor only; device metadata keeps positions_h_).
-  std::vector<int32_t> locations_h_, requests_h_, positions_h_, mapping_h_, max_position_;
+  std::vector<int32_t> locations_h_, requests_h_, positions_h_, max_position_;
+  HostWords mapping_h_;  // the request map as constructed (host constructor only)
   std::vector<Sequence> sequences_;
   // row_context_: visible keys of each row (its position + 1), the decode
   // kernel's row_context when every row is a decode row.

@@ -49,6 +49,11 @@ probability or a sum differently (max abs 9.8e-4, mean abs at most 6e-7).
   host constructor's accept/reject decision on random corruptions. Code 5
   (position != prefix + offset) has no reference test vector: parity unpinned
   beyond the brute force.
+- ``host_metadata_error``: the host constructor cases of the reference's
+  tests/paged_metadata_smoke.py:33-50 on that test's data, the precedence its
+  loops impose (map range, then rows, then prefixes by request and position),
+  and agreement with ``metadata_codes`` on random sequence layouts
+  (tests/test_oracle_metadata.py).
 - ``page_flags`` / ``largest_page``: closed forms (identity map -> 1024, a map
   shifted by one slot -> 1, permuted pages of P -> P) and brute force over
   random block tables.
@@ -483,6 +488,43 @@ def metadata_codes(locations, batch_requests, positions, mapping, prefixes, leng
         if codes[i] == 0 and (missing or aliased):
             codes[i] = 6 if missing else 7
     return codes
+
+
+def host_metadata_error(locations, requests, positions, mapping, slots):
+    """The failure the reference's host PagedMetadata constructor reports
+    (src/bridge/paged_metadata.cpp:82-139), as its message fragment, or None.
+
+    Checks in the reference's order, the first failing one reported: every
+    request-map entry in [-1, slots) (:103-107); then row by row (:110-130)
+    location, request and position in range, mapping[request, position] ==
+    location, and no earlier row with the same location; then request by
+    request, every position up to the request's last row (:131-139) has a
+    slot (>= 0) that no other (request, position) row writes. Dimensions are
+    assumed valid (:91-94)."""
+    mapping = np.asarray(mapping)
+    request_count, context = mapping.shape
+    locations, requests, positions = _ints(locations), _ints(requests), _ints(positions)
+    if any(not -1 <= int(v) < slots for v in mapping.reshape(-1)):
+        return "request-to-token slot is out of range"
+    targets = {}
+    last = [-1] * request_count
+    for loc, req, pos in zip(locations, requests, positions):
+        if not (0 <= loc < slots and 0 <= req < request_count and 0 <= pos < context):
+            return "paged metadata index is out of range"
+        if int(mapping[req, pos]) != loc:
+            return "output slot does not match request-to-token mapping"
+        if loc in targets:
+            return "duplicate output KV slot"
+        targets[loc] = (req, pos)
+        last[req] = max(last[req], pos)
+    for req in range(request_count):
+        for t in range(last[req] + 1):
+            slot = int(mapping[req, t])
+            if slot < 0:
+                return "missing KV slot in a visible prefix"
+            if targets.get(slot, (req, t)) != (req, t):
+                return "output KV slot aliases another visible prefix position"
+    return None
 
 
 def page_flags(mapping, batch_requests, prefixes, lengths):

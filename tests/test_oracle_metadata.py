@@ -7,7 +7,9 @@ tests/paged_attention_generalized_smoke.py:146-158 and
 tests/dynamic_eager_ops_smoke.py:383-418, evaluated here as literal lists.
 The accept/reject decision is also checked against a set-based brute force of
 the host constructor's rules (src/bridge/paged_metadata.cpp:82-138) on random
-corruptions.
+corruptions. The host constructor's reported failure (host_metadata_error) is
+pinned by the reference's tests/paged_metadata_smoke.py cases, by the order
+its loops impose, and against the device codes on random layouts.
 """
 
 import numpy as np
@@ -128,6 +130,99 @@ def test_accept_reject_matches_brute_force():
         assert (first_error(codes) is None) == accept, (trial, codes)
         outcomes.update(set(codes))
     assert outcomes == {0, 1, 2, 3, 4, 5, 6, 7}, outcomes
+
+
+def reference_smoke_metadata(rows):
+    """tests/paged_metadata_smoke.py:14-19 of the reference (192 slots)."""
+    mapping = np.arange(192, dtype=np.int32).reshape(3, 64)
+    requests = np.arange(rows, dtype=np.int64) % 3
+    positions = np.arange(rows, dtype=np.int64) // 3 + 2
+    return mapping[requests, positions].astype(np.int64), requests, positions, mapping
+
+
+def test_host_metadata_error_reference_smoke():
+    """Known answers: the host constructor cases of the reference's
+    tests/paged_metadata_smoke.py:33-50, on that test's data."""
+    for rows in (1, 3, 17, 137):
+        assert orc.host_metadata_error(*reference_smoke_metadata(rows), 192) is None
+    locations, requests, positions, mapping = reference_smoke_metadata(7)
+    duplicate, dup_requests, dup_positions = locations.copy(), requests.copy(), positions.copy()
+    duplicate[1], dup_requests[1], dup_positions[1] = duplicate[0], requests[0], positions[0]
+    assert orc.host_metadata_error(duplicate, dup_requests, dup_positions, mapping, 192) == "duplicate output KV slot"
+    invalid = locations.copy()
+    invalid[0] = 192
+    assert "out of range" in orc.host_metadata_error(invalid, requests, positions, mapping, 192)
+    missing = mapping.copy()
+    missing[0, 0] = -1
+    assert "missing KV slot" in orc.host_metadata_error(locations, requests, positions, missing, 192)
+    alias = mapping.copy()
+    alias[1, 0] = locations[0]
+    assert "aliases another visible prefix" in orc.host_metadata_error(locations, requests, positions, alias, 192)
+    mismatch = mapping.copy()
+    mismatch[requests[0], positions[0]] = 191
+    assert "does not match" in orc.host_metadata_error(locations, requests, positions, mismatch, 192)
+
+
+def test_host_metadata_error_order():
+    """The first failure in the reference's order is the one reported: the map
+    range before any row, rows in order (range, agreement, repeat), then
+    prefixes request by request and position by position."""
+    locations, requests, positions, mapping = reference_smoke_metadata(7)
+    err = lambda loc=locations, req=requests, pos=positions, mp=mapping: orc.host_metadata_error(  # noqa: E731
+        loc, req, pos, mp, 192)
+    beyond = mapping.copy()
+    beyond[2, 63] = 192  # outside every prefix
+    bad_loc = locations.copy()
+    bad_loc[3] = 5
+    assert err(mp=beyond, loc=bad_loc) == "request-to-token slot is out of range"
+    assert err(loc=bad_loc) == "output slot does not match request-to-token mapping"
+    hole = mapping.copy()
+    hole[0, 0] = -1
+    assert err(loc=bad_loc, mp=hole) == "output slot does not match request-to-token mapping"
+    # request 0 aliases at position 1, request 1 misses position 0: request 0 first
+    both = mapping.copy()
+    both[0, 1] = locations[1]
+    both[1, 0] = -1
+    assert err(mp=both) == "output KV slot aliases another visible prefix position"
+    # within one request the earlier position wins
+    both = mapping.copy()
+    both[1, 0] = -1
+    both[1, 1] = locations[0]
+    assert err(mp=both) == "missing KV slot in a visible prefix"
+    # a row's own output slot at its own position is not an alias
+    assert err() is None
+
+
+def test_host_metadata_error_agrees_with_device_codes():
+    """On sequence layouts (no position off the layout, code 5), the host
+    constructor accepts exactly the rows the device validation gives no code."""
+    rng = np.random.default_rng(43)
+    seen = set()
+    for trial in range(300):
+        requests_n, context, slots = 4, 24, 200
+        mapping = rng.permutation(slots)[: requests_n * context].reshape(requests_n, context).astype(np.int32)
+        batch = int(rng.integers(1, 4))
+        batch_requests = rng.permutation(requests_n)[:batch].astype(np.int64)
+        prefixes = [int(rng.integers(0, 12)) for _ in range(batch)]
+        lengths = [int(rng.integers(1, 6)) for _ in range(batch)]
+        row_req = np.repeat(batch_requests, lengths)
+        positions = np.concatenate([np.arange(p, p + n) for p, n in zip(prefixes, lengths)]).astype(np.int64)
+        locations = mapping[row_req, positions].astype(np.int64)
+        r = int(rng.integers(0, len(locations)))
+        kind = trial % 5
+        if kind == 1:
+            locations[r] = mapping[row_req[r], (positions[r] + 1) % context]
+        elif kind == 2:
+            mapping[batch_requests[0], int(rng.integers(0, prefixes[0] + 1))] = -1
+        elif kind == 3:
+            mapping[(batch_requests[0] + 1) % requests_n, 0] = locations[r]
+        elif kind == 4:
+            locations[r] = slots + int(rng.integers(0, 3))
+        codes = orc.metadata_codes(locations, batch_requests, positions, mapping, prefixes, lengths, slots)
+        error = orc.host_metadata_error(locations, row_req, positions, mapping, slots)
+        assert (error is None) == (first_error(codes) is None), (trial, codes, error)
+        seen.add(error)
+    assert len(seen) >= 4, seen
 
 
 def test_page_flags_closed_forms():

@@ -6,6 +6,7 @@ Message fragments follow the reference's host constructor
 (tests/paged_metadata_smoke.py:38-54 of the reference).
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -116,6 +117,103 @@ def test_metadata_rejections(case, fragment):
         mapping[1, 0] = int(mapping[0, 2])
     with pytest.raises(RuntimeError, match=fragment):
         _meta(locations, requests, positions, mapping, slots)
+
+
+def _host_outcome(locations, requests, positions, mapping, slots):
+    """None when the host constructor's validation passes (it then goes on to
+    the device, which this container does not have), else the error text."""
+    try:
+        torch.classes.gaudirt.PagedMetadata(locations, requests, positions, mapping, slots)
+    except RuntimeError as error:
+        text = str(error)
+        return None if "no current HIP device" in text else text
+    return None
+
+
+def _paged_problem(rng, page):
+    requests_n = int(rng.integers(1, 7))
+    context = int(rng.integers(16, 300))
+    pages = -(-context // page)
+    blocks = rng.permutation(requests_n * pages + 8)[: requests_n * pages].reshape(requests_n, pages)
+    slots = (requests_n * pages + 8) * page
+    t = np.arange(context)
+    visible = rng.integers(1, context + 1, requests_n)
+    mapping = np.where(t[None, :] < visible[:, None], blocks[:, t // page] * page + t % page, -1)
+    chosen = rng.permutation(requests_n)[: int(rng.integers(1, requests_n + 1))]
+    rows = []
+    for request in chosen:
+        length = int(rng.integers(1, min(6, int(visible[request])) + 1))
+        first = int(rng.integers(0, int(visible[request]) - length + 1))
+        rows += [(int(request), first + k) for k in range(length)]
+    order = rng.permutation(len(rows))
+    requests = np.array([rows[i][0] for i in order], dtype=np.int64)
+    positions = np.array([rows[i][1] for i in order], dtype=np.int64)
+    locations = mapping[requests, positions].astype(np.int64)
+    return locations, requests, positions, mapping.astype(np.int32), slots
+
+
+def _plant(rng, kind, problem):
+    locations, requests, positions, mapping, slots = problem
+    locations, requests, positions, mapping = locations.copy(), requests.copy(), positions.copy(), mapping.copy()
+    last = {int(r): int(positions[requests == r].max()) for r in np.unique(requests)}
+    i = int(rng.integers(0, len(locations)))
+    victim = int(rng.choice(list(last)))
+    if kind == "missing":
+        mapping[victim, int(rng.integers(0, last[victim] + 1))] = -1
+    elif kind == "alias":  # a written slot anywhere in some visible prefix
+        mapping[victim, int(rng.integers(0, last[victim] + 1))] = locations[i]
+    elif kind == "alias_run":  # a whole page holding a written slot, inside a run
+        page = int(rng.choice([4, 8, 16]))
+        start = int(rng.integers(0, last[victim] + 1)) // page * page
+        block = int(locations[i]) // page * page
+        end = min(start + page, mapping.shape[1])
+        mapping[victim, start:end] = block + np.arange(end - start)
+    elif kind == "map_range":
+        mapping[int(rng.integers(0, mapping.shape[0])), int(rng.integers(0, mapping.shape[1]))] = \
+            [slots, -2, slots + 7][int(rng.integers(0, 3))]
+    elif kind == "mismatch":
+        locations[i] = (locations[i] + 1) % slots
+    elif kind == "duplicate":
+        j = int(rng.integers(0, len(locations)))
+        locations, requests, positions = (np.append(a, a[j]) for a in (locations, requests, positions))
+    elif kind == "index":
+        positions[i] = mapping.shape[1]
+    return locations, requests, positions, mapping, slots
+
+
+def test_host_constructor_matches_oracle():
+    """The host constructor reports what the reference's constructor would
+    (oracle.host_metadata_error: same failure, same order) on random paged and
+    token-granular maps, with one or two planted faults: missing and aliased
+    prefix slots (also inside a run of consecutive slots), out-of-range map
+    entries, rows off the map, repeated rows and out-of-range indices."""
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(2024)
+    kinds = ["none", "missing", "alias", "alias_run", "map_range", "mismatch", "duplicate", "index"]
+    seen = set()
+    for trial in range(480):
+        page = [1, 4, 8, 16, 64][trial % 5]
+        problem = _paged_problem(rng, page)
+        planted = [kinds[(trial // 5) % len(kinds)]]
+        if trial % 3 == 0:
+            planted.append(kinds[int(rng.integers(1, len(kinds)))])
+        for kind in planted:
+            if kind != "none":
+                problem = _plant(rng, kind, problem)
+        locations, requests, positions, mapping, slots = problem
+        want = orc.host_metadata_error(locations, requests, positions, mapping, slots)
+        as_tensor = lambda a, dtype: torch.from_numpy(np.ascontiguousarray(a.astype(dtype)))  # noqa: E731
+        map_dtype = np.int64 if trial % 4 == 1 else np.int32
+        got = _host_outcome(as_tensor(locations, np.int64), as_tensor(requests, np.int64),
+                            as_tensor(positions, np.int32 if trial % 2 else np.int64), as_tensor(mapping, map_dtype),
+                            slots)
+        if want is None:
+            assert got is None, (trial, planted, got)
+        else:
+            assert got is not None and want in got, (trial, planted, want, got)
+        seen.add(want)
+    assert len(seen) == 7, seen
 
 
 def test_fake_kernels_on_meta_tensors():
