@@ -14,9 +14,11 @@ HIP events on the launch stream, and the CPU baseline (the C oracle, a
 restatement of the reference's direct_bf16_pv, on the host's cores). With the
 default headline workload (c2) the same line carries `secondary`: the other
 GPU configurations (c3 fused store + decode, c5 long-context decode: HBM
-roofline; c4 prefix-shared prefill: MFMA roofline), each timed the same way in
-the same process right after the headline, `--steps` steps each (c3 and c5
-after at least 100 warm-up steps, c4 after 1000); the CPU baseline runs last.
+roofline; c4 prefix-shared prefill: MFMA roofline), each timed the same way,
+`--steps` steps each (c3 and c5 after at least 100 warm-up steps, c4 after
+1000), right after the headline, each by a child `bench.py --workload` process
+of its own (a pool allocated after others were released ran ~4% slower); the
+CPU baseline runs last.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20 (c4: 1000)] [--workload c2] [--no-cpu]
                     [--no-secondary] [--host-overhead]
@@ -309,33 +311,38 @@ def decode_run(lib, workload, steps, warmup, table_sets, seed, partition):
     }
 
 
-def secondary_runs(lib, args):
-    """C3, C5 (HBM roofline) and C4 (MFMA roofline) after the headline, in the same
-    process, `args.steps` timed steps each."""
-    import torch
+def secondary_runs(args):
+    """C3, C5 (HBM roofline) and C4 (MFMA roofline) after the headline, each timed
+    over `args.steps` steps by a child `bench.py --workload <w>` process whose JSON
+    line is read back. A decode case set up in a process that had already
+    allocated and released multi-GiB pools ran about 4% slower (the second of
+    C3 / C5 in one process: C5 210.6 vs 202.4 us, C3 194.9 vs 187.8), so each
+    case gets a process of its own, as a server allocates its pool once."""
+    import subprocess
 
     out = {}
-    warmup = max(args.warmup, 100)  # the first calls of a new case page in its pool and tables
-    for workload in ("c3", "c5"):
-        r = decode_run(lib, workload, args.steps, warmup, args.table_sets, args.seed, 0)
-        dc = r.pop("case")
-        out[workload] = {
-            "workload": f"{workload}: {WORKLOADS[workload]}",
-            "value": r["tokens_per_s"], "unit": "tokens/s", "ms_per_step": r["ms_per_step"],
-            "steps": args.steps, "warmup": warmup, "split_k_partition": r["partition"],
-            "mean_context": float(dc.lens.mean()), "max_context": int(dc.lens.max()),
-            "roofline": r["roofline"],
-        }
-        del dc
-        torch.cuda.empty_cache()
-    ms, tflops, pc = prefill_run(lib, args.steps, C4_WARMUP, args.seed)
-    out["c4"] = {
-        "workload": f"c4: {WORKLOADS['c4']}",
-        "value": tflops, "unit": "TFLOP/s", "ms_per_step": ms, "steps": args.steps, "warmup": C4_WARMUP,
-        "flops_per_step": pc.flops(), "roofline": prefill_roofline(tflops),
-    }
-    del pc
-    torch.cuda.empty_cache()
+    for workload in ("c3", "c5", "c4"):
+        # The first calls of a new case page in its pool and tables; C4's
+        # MFMA-bound kernel also needs the clocks up.
+        warmup = C4_WARMUP if workload == "c4" else max(args.warmup, 100)
+        cmd = [sys.executable, "-u", os.path.abspath(__file__), "--workload", workload, "--no-cpu", "--no-secondary",
+               "--steps", str(args.steps), "--warmup", str(warmup), "--seed", str(args.seed),
+               "--table-sets", str(args.table_sets)]
+        proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=900)
+        sys.stderr.write(proc.stderr)
+        sys.stderr.flush()
+        if proc.returncode != 0:
+            raise RuntimeError(f"bench.py: the {workload} leg exited with status {proc.returncode}")
+        line = json.loads(proc.stdout.strip().splitlines()[-1])
+        entry = {"workload": line["config"]["workload"], "value": line["value"], "unit": line["unit"],
+                 "ms_per_step": line["ms_per_step"], "steps": line["steps"], "warmup": line["warmup"]}
+        if workload == "c4":
+            entry["flops_per_step"] = line["config"]["flops_per_step"]
+        else:
+            entry.update(split_k_partition=line["config"]["split_k_partition"],
+                         mean_context=line["config"]["mean_context"], max_context=line["config"]["max_context"])
+        entry["roofline"] = line["roofline"]
+        out[workload] = entry
     return out
 
 
@@ -449,7 +456,7 @@ def main():
     # work with the GPU idle) comes last.
     secondary = None
     if args.workload == "c2" and not args.no_secondary:
-        secondary = secondary_runs(lib, args)
+        secondary = secondary_runs(args)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(dc, args.cpu_seconds)

@@ -22,6 +22,10 @@ GK_ERR_OUT_OF_MEMORY = 4
 GK_ERR_WORKSPACE = 5
 GK_DECODE_SCRATCH_BYTES = 32 << 20
 GK_METADATA_INLINE_WORDS = 768
+# Fixed cost per work unit of the balanced decode schedule, in tiles
+# (GK_STREAM_UNIT_COST of gaudirt_amd/csrc/work_order.hpp); it enters the
+# schedule's 2^31 gate.
+STREAM_UNIT_COST = 2
 
 # Every function include/gaudirt_amd.h declares.
 EXPORTED = [

@@ -2,12 +2,16 @@
 //
 // The grid holds exactly as many one-wave workgroups as the GPU keeps resident.
 // All key tiles of the batch form one sequence: work units (row, kv head, head
-// group) in row-major order, each unit's tiles in key order. Workgroup w takes
-// the contiguous range [w * per, (w + 1) * per) of that sequence, so every
-// workgroup streams the same number of K/V bytes however skewed the context
-// lengths are, and its two-stage LDS pipeline runs without a break from its
-// first tile to its last: crossing into the next unit only swaps the query
-// (prefetched into LDS with that unit's first tile) and the softmax state.
+// group) in row-major order, each unit's tiles in key order, each unit
+// preceded by kStreamUnitCost positions that stand for its fixed cost (the
+// finish of a unit: its stores, which hold up the next tile wait, and a new
+// query). Workgroup w takes the contiguous range [w * per, (w + 1) * per) of
+// those positions, so every workgroup streams about the same number of K/V
+// bytes however skewed the context lengths are, a few tiles fewer for each
+// unit it crosses, and its two-stage LDS pipeline runs without a break from
+// its first tile to its last: crossing into the next unit only swaps the
+// query (prefetched into LDS with that unit's first tile) and the softmax
+// state.
 //
 // A unit whose tiles all fall in one workgroup is finalised there (bf16
 // output). A unit that spans workgroups w_first .. w_last leaves one partial
@@ -183,11 +187,11 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   int lane_tiles = 0;
 #pragma unroll
   for (int k = 0; k < kPre; ++k)
-    if (64 * k + lane < a.rows) lane_tiles += row_tiles<TS>(pctx[k], a.window).count;
+    if (64 * k + lane < a.rows) lane_tiles += row_tiles<TS>(pctx[k], a.window).count + kStreamUnitCost;
   int64_t total = wave_sum(lane_tiles);
   for (int base = 64 * kPre; base < a.rows; base += 64) {
     const int r = base + lane;
-    total += wave_sum(r < a.rows ? row_tiles<TS>(a.row_context[r], a.window).count : 0);
+    total += wave_sum(r < a.rows ? row_tiles<TS>(a.row_context[r], a.window).count + kStreamUnitCost : 0);
   }
   total *= U;
   // The tile sequence is numbered in 32 bits from here on (fewer scalar
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   const int g_end = min(g_begin + per, (int)total);
   if (g_begin >= g_end) return;
 
-  // The row holding tile g_begin, and the sequence index of its first tile.
+  // The row holding position g_begin, and the position of its first unit.
   int row = 0;
   int row_base = 0;
   int pre = 0;
@@ -222,7 +226,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   for (int k = 0; k < kPre; ++k) {
     if (found || 64 * k >= a.rows) continue;
     const int r = 64 * k + lane;
-    const int n = r < a.rows ? row_tiles<TS>(pctx[k], a.window).count : 0;
+    const int n = r < a.rows ? row_tiles<TS>(pctx[k], a.window).count + kStreamUnitCost : 0;
     const int incl = wave_inclusive_scan(n);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(r < a.rows && (pre + incl) * U > g_begin);
     if (hit) {
@@ -237,7 +241,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   for (int base = 64 * kPre; !found && base < a.rows; base += 64) {
     load_window(base);
     const int r = base + lane;
-    const int n = r < a.rows ? row_tiles<TS>(wctx, a.window).count : 0;
+    const int n = r < a.rows ? row_tiles<TS>(wctx, a.window).count + kStreamUnitCost : 0;
     const int incl = wave_inclusive_scan(n);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(r < a.rows && (pre + incl) * U > g_begin);
     if (hit) {
@@ -266,10 +270,12 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     cur.rt = row_tiles<TS>(__builtin_amdgcn_readlane(wctx, l), a.window);
     cur.req = __builtin_amdgcn_readlane(wreq, l);
     cur.qrow = __builtin_amdgcn_readlane(wmap, l);
-    const int off = g_begin - row_base;  // below U * count
-    cur.h = (int)((uint32_t)off / (uint32_t)cur.rt.count);
-    cur.j = off - cur.h * cur.rt.count;
-    cur.g = g_begin;
+    // A share that starts inside a unit's fixed cost starts at its first tile.
+    const StreamStart st = stream_start((uint32_t)(g_begin - row_base), (uint32_t)(cur.rt.count + kStreamUnitCost),
+                                        kStreamUnitCost);
+    cur.h = st.h;
+    cur.j = st.j;
+    cur.g = g_begin + st.skip;
     enter_unit(cur);
     cur.next_ctx = cur.next_req = cur.next_qrow = 0;
     if (row + 1 < a.rows) {
@@ -278,10 +284,12 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       cur.next_qrow = a.row_map ? scalar_load(a.row_map, row + 1) : row + 1;
     }
   }
+  if (cur.g >= g_end) return;  // the share holds only a unit's fixed cost
   auto advance = [&](Cursor& c) {
     ++c.g;
     if (++c.j < c.rt.count) return;
     c.j = 0;
+    c.g += kStreamUnitCost;
     if (++c.h < U) {
       enter_unit(c);
       return;
@@ -650,8 +658,9 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   };
 
   // ---- Pipeline ------------------------------------------------------------
-  // Stage 0 / stage 1 alternate; the query buffer alternates per unit.
-  int to_issue = g_end - g_begin;  // tiles not yet issued
+  // Stage 0 / stage 1 alternate; the query buffer alternates per unit. The
+  // share ends at the position g_end: `ahead` says whether the cursor, one
+  // tile past the last issued one, is still inside it.
   int qpar = 0;
   TileEntries<NR> first_entry = table_entry(cur);
   pack(first_entry);
@@ -659,15 +668,15 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   int qp0 = 0, qp1 = 0;                // query buffer of the tile in stage 0 / 1
   if (d0.flags & kTileFirst) issue_query(d0, qs[0]);
   issue_tile(d0, first_entry, kt0, vt0);
-  --to_issue;
+  advance(cur);
+  bool ahead = cur.g < g_end;
   TileEntries<NR> next_entry = {};
-  if (to_issue > 0) {
-    advance(cur);
+  if (ahead) {
     next_entry = table_entry(cur);
     pack(next_entry);
   }
   while (true) {
-    bool more = to_issue > 0;
+    bool more = ahead;
     if (more) {
       d1 = describe(cur, next_entry);
       if (d1.flags & kTileFirst) {
@@ -676,10 +685,9 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       }
       qp1 = qpar;
       issue_tile(d1, next_entry, kt1, vt1);
-      if (--to_issue > 0) {
-        advance(cur);
-        next_entry = table_entry(cur);
-      }
+      advance(cur);
+      ahead = cur.g < g_end;
+      if (ahead) next_entry = table_entry(cur);
       wait_vmem<2 * S::LOADS>();
       pack(next_entry);  // its scalar loads landed during the wait
     } else {
@@ -688,7 +696,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     consume(d0, kt0, vt0, qp0);
     if (!more) break;
 
-    more = to_issue > 0;
+    more = ahead;
     if (more) {
       d0 = describe(cur, next_entry);
       if (d0.flags & kTileFirst) {
@@ -697,10 +705,9 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       }
       qp0 = qpar;
       issue_tile(d0, next_entry, kt0, vt0);
-      if (--to_issue > 0) {
-        advance(cur);
-        next_entry = table_entry(cur);
-      }
+      advance(cur);
+      ahead = cur.g < g_end;
+      if (ahead) next_entry = table_entry(cur);
       wait_vmem<2 * S::LOADS>();
       pack(next_entry);  // its scalar loads landed during the wait
     } else {

@@ -84,13 +84,37 @@ constexpr int stream_row_tile_count(int ctx, int window, int ts) {
   return c > 0 ? (c + ts - 1) / ts - visible_left(c, window) / ts : 1;
 }
 
-// The balanced schedule numbers the tiles of a whole batch (units * tiles of
-// each row) in 32 bits, and its kernel splits them over `wgs` workgroups with
-// (total + wgs - 1) / wgs: total + wgs must stay below 2^31. With every
-// row_context <= max_context a row has at most max_context / ts + 2 tiles, so
-// the host runs the schedule only when this holds.
+// Fixed cost of a work unit in the balanced schedule, in tiles: a unit of n
+// tiles takes n + kStreamUnitCost positions of the schedule's numbering (the
+// cost first, then its tiles), so that a workgroup whose share crosses many
+// short units (each one a finish with its stores, and a new query) is given
+// fewer tiles. 0 numbers the tiles alone.
+#ifndef GK_STREAM_UNIT_COST
+#define GK_STREAM_UNIT_COST 2
+#endif
+constexpr int kStreamUnitCost = GK_STREAM_UNIT_COST;
+
+// Where a workgroup starts whose share begins `off` positions into a row's
+// units (`weight` = tiles + cost positions each): unit h, tile j, after
+// passing over `skip` positions of that unit's cost.
+struct StreamStart {
+  int h, j, skip;
+};
+constexpr StreamStart stream_start(uint32_t off, uint32_t weight, int cost) {
+  const int h = (int)(off / weight);
+  const int jw = (int)(off - (uint32_t)h * weight);
+  return jw < cost ? StreamStart{h, 0, cost - jw} : StreamStart{h, jw - cost, 0};
+}
+
+// The balanced schedule numbers the positions of a whole batch (units *
+// (tiles + cost) of each row) in 32 bits, and its kernel splits them over
+// `wgs` workgroups with (total + wgs - 1) / wgs: total + wgs must stay below
+// 2^31. With every row_context <= max_context a row has at most
+// max_context / ts + 2 tiles, so the host runs the schedule only when this
+// holds.
 constexpr bool stream_tiles_fit(int64_t units, int64_t max_context, int ts, int64_t wgs) {
-  return units >= 0 && max_context >= 0 && wgs >= 1 && units * (max_context / ts + 2) + wgs < (int64_t(1) << 31);
+  return units >= 0 && max_context >= 0 && wgs >= 1 &&
+         units * (max_context / ts + 2 + kStreamUnitCost) + wgs < (int64_t(1) << 31);
 }
 
 }  // namespace gk

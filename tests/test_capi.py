@@ -132,6 +132,11 @@ def test_metadata_and_allocator_validation(lib):
     assert rc == capi.GK_ERR_WORKSPACE
 
 
+def test_stream_unit_cost_matches_the_header():
+    source = (ROOT / "gaudirt_amd" / "csrc" / "work_order.hpp").read_text()
+    assert re.search(r"#define GK_STREAM_UNIT_COST (\d+)", source).group(1) == str(capi.STREAM_UNIT_COST)
+
+
 def test_metadata_staged_words_validation(lib):
     """Staged-word arguments are refused before any launch: missing pointers,
     more than GK_METADATA_INLINE_WORDS words, an input only partly inside the

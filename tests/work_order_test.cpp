@@ -1,8 +1,9 @@
-// CPU check of gk::heavy_first_item (gaudirt_amd/csrc/work_order.hpp), the
-// prefill kernel's order of work items inside one XCD's share. For every
-// share of many launch shapes it checks what the order must be: a
-// permutation of the share, row tiles non-increasing, ascending items within
-// one row tile. Prints OK on success.
+// CPU checks of gaudirt_amd/csrc/work_order.hpp: gk::heavy_first_item, the
+// prefill kernel's order of work items inside one XCD's share (for every
+// share of many launch shapes: a permutation of the share, row tiles
+// non-increasing, ascending items within one row tile); gk::fast_div; the
+// balanced decode schedule's tile counts, 2^31 gate and split with per-unit
+// fixed cost (gk::stream_start). Prints OK on success.
 #include <algorithm>
 #include <cstdio>
 #include <vector>
@@ -114,8 +115,9 @@ void check_stream_gate() {
       for (int64_t units : {int64_t(1), int64_t(7), int64_t(1023), int64_t(65535), int64_t(65535) * 8 * 4}) {
         // The largest per-row tile bound n = max_context / ts + 2 the gate admits.
         const int64_t n_max = (limit - 1 - wgs) / units;
-        if (n_max < 2) continue;
-        const int64_t mc_fit = (n_max - 2) * ts + ts - 1, mc_over = (n_max - 1) * ts;
+        const int64_t fixed = 2 + gk::kStreamUnitCost;  // n = max_context / ts + fixed
+        if (n_max < fixed) continue;
+        const int64_t mc_fit = (n_max - fixed) * ts + ts - 1, mc_over = (n_max - fixed + 1) * ts;
         if (!gk::stream_tiles_fit(units, mc_fit, ts, wgs) || gk::stream_tiles_fit(units, mc_over, ts, wgs)) {
           if (failures++ < 10)
             std::printf("ts=%d wgs=%lld units=%lld: gate boundary not at max_context %lld / %lld\n", ts,
@@ -125,7 +127,7 @@ void check_stream_gate() {
         if (mc_fit > 0x7fffffff) continue;  // row_context is int32
         // Every row at mc_fit under the windows that maximise its tiles.
         for (int window : {0, ts - 1, ts + 1, 2 * ts - 1, (int)std::min<int64_t>(mc_fit, 0x7fffffff)}) {
-          const int64_t total = units * gk::stream_row_tile_count((int)mc_fit, window, ts);
+          const int64_t total = units * (gk::stream_row_tile_count((int)mc_fit, window, ts) + gk::kStreamUnitCost);
           if (total + wgs >= limit) {
             if (failures++ < 10)
               std::printf("ts=%d wgs=%lld units=%lld window=%d: gate passed but total %lld + wgs reaches 2^31\n", ts,
@@ -143,11 +145,104 @@ void check_stream_gate() {
   }
 }
 
+// The balanced decode schedule as the kernel walks it: rows of `units_per_row`
+// units with tiles[row] tiles each, every unit preceded by `cost` positions of
+// fixed cost, the numbering split over `wgs` workgroups. Checks that every
+// tile of every unit is visited exactly once and in order, that a workgroup
+// starting inside a unit's cost starts at its first tile, and that the
+// partial slots the workgroups write for a split unit are the ones the merge
+// reads for it (first part 2 wf + (g0 == wf per ? 0 : 1), then 2 w for each
+// later workgroup w, wf = g0 / per, g0 the position of the unit's first tile).
+void check_stream_schedule(const std::vector<int>& tiles, int units_per_row, int wgs, int cost) {
+  const int rows = (int)tiles.size(), U = units_per_row, units = rows * U;
+  std::vector<int64_t> start(units + 1, 0);  // position of each unit's cost
+  for (int u = 0; u < units; ++u) start[u + 1] = start[u] + tiles[u / U] + cost;
+  const int64_t total = start[units];
+  const int64_t per = (total + wgs - 1) / wgs;
+  std::vector<int> visited(units, 0), first_wg(units, -1), last_wg(units, -1);
+  std::vector<std::vector<int>> slots(units);
+  auto fail = [&](const char* what, int w, int u) {
+    if (failures++ < 10)
+      std::printf("schedule rows=%d U=%d wgs=%d cost=%d: %s (workgroup %d, unit %d)\n", rows, U, wgs, cost, what, w, u);
+  };
+  for (int w = 0; w < wgs; ++w) {
+    const int64_t g_begin = w * per, g_end = std::min(g_begin + per, total);
+    if (g_begin >= g_end) continue;
+    int row = 0;
+    while ((int64_t)(row + 1) * U <= units && start[(row + 1) * U] <= g_begin) ++row;
+    const gk::StreamStart st =
+        gk::stream_start(uint32_t(g_begin - start[row * U]), uint32_t(tiles[row] + cost), cost);
+    int h = st.h, j = st.j;
+    int64_t g = g_begin + st.skip;
+    if (st.h >= U || (st.skip > 0 && st.j != 0)) return fail("start outside the row", w, row * U);
+    while (g < g_end) {
+      const int u = row * U + h, count = tiles[row];
+      if (g != start[u] + cost + j) return fail("position does not match the tile", w, u);
+      if (visited[u] != j) return fail("tile visited out of order or twice", w, u);
+      ++visited[u];
+      if (j == 0) first_wg[u] = w;
+      if (j == count - 1) last_wg[u] = w;
+      const bool seg_end = j == count - 1 || g == g_end - 1;
+      if (seg_end) {
+        const int64_t g0 = g - j;
+        const bool whole = g0 >= g_begin && g0 + count <= g_end;
+        if (!whole) slots[u].push_back(2 * w + (g0 <= g_begin ? 0 : 1));
+      }
+      ++g;
+      if (++j == count) {
+        j = 0;
+        g += cost;
+        if (++h == U) h = 0, ++row;
+        if (row >= rows) break;
+      }
+    }
+  }
+  for (int u = 0; u < units; ++u) {
+    if (visited[u] != tiles[u / U]) return fail("unit not fully visited", -1, u);
+    const int64_t g0 = start[u] + cost;
+    const int wf = (int)(g0 / per);
+    if (first_wg[u] != wf) return fail("first tile not in workgroup g0 / per", first_wg[u], u);
+    if (first_wg[u] == last_wg[u]) {
+      if (!slots[u].empty()) return fail("whole unit left a partial", first_wg[u], u);
+      continue;
+    }
+    const int first_slot = 2 * wf + (g0 == wf * per ? 0 : 1);
+    const int nparts = last_wg[u] - wf + 1;
+    if ((int)slots[u].size() != nparts) return fail("partial count differs from the span", wf, u);
+    for (int k = 0; k < nparts; ++k)
+      if (slots[u][k] != (k == 0 ? first_slot : 2 * (wf + k))) return fail("partial slot differs from the merge's", wf + k, u);
+  }
+}
+
+void check_stream_schedules() {
+  uint64_t state = 0x243f6a8885a308d3ull;
+  auto next = [&](int n) {
+    state ^= state << 13, state ^= state >> 7, state ^= state << 17;
+    return int(state % uint64_t(n));
+  };
+  for (int cost = 0; cost <= 3; ++cost) {
+    for (int trial = 0; trial < 400; ++trial) {
+      const int rows = 1 + next(40), U = 1 + next(8), wgs = 1 + next(96);
+      std::vector<int> tiles(rows);
+      for (int& t : tiles) t = 1 + (next(4) == 0 ? next(200) : next(6));
+      check_stream_schedule(tiles, U, wgs, cost);
+    }
+    // C2-, C3- and C5-like shapes at 1024 workgroups.
+    for (int shape = 0; shape < 3; ++shape) {
+      const int rows = shape == 0 ? 64 : shape == 1 ? 256 : 32;
+      std::vector<int> tiles(rows);
+      for (int& t : tiles) t = shape == 0 ? 16 + next(113) : shape == 1 ? 4 + next(61) : 32 + next(993);
+      check_stream_schedule(tiles, 8, 1024, cost);
+    }
+  }
+}
+
 }  // namespace
 
 int main() {
   check_fast_div();
   check_stream_gate();
+  check_stream_schedules();
   // C4: 8 sequences x 8 kv heads x 8 row tiles.
   check_launch(512, 8);
   // Every small shape, every alignment of a share against the row tiles.
