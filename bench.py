@@ -328,11 +328,17 @@ def secondary_runs(args):
         cmd = [sys.executable, "-u", os.path.abspath(__file__), "--workload", workload, "--no-cpu", "--no-secondary",
                "--steps", str(args.steps), "--warmup", str(warmup), "--seed", str(args.seed),
                "--table-sets", str(args.table_sets)]
-        proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=900)
+        try:
+            proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=900)
+        except subprocess.TimeoutExpired:
+            out[workload] = {"error": "timed out after 900 s"}
+            continue
         sys.stderr.write(proc.stderr)
         sys.stderr.flush()
-        if proc.returncode != 0:
-            raise RuntimeError(f"bench.py: the {workload} leg exited with status {proc.returncode}")
+        if proc.returncode != 0 or not proc.stdout.strip():
+            # The headline stands on its own: a failed leg is reported, not raised.
+            out[workload] = {"error": f"exited with status {proc.returncode}"}
+            continue
         line = json.loads(proc.stdout.strip().splitlines()[-1])
         entry = {"workload": line["config"]["workload"], "value": line["value"], "unit": line["unit"],
                  "ms_per_step": line["ms_per_step"], "steps": line["steps"], "warmup": line["warmup"]}

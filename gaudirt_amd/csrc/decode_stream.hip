@@ -194,13 +194,13 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     total += wave_sum(r < a.rows ? row_tiles<TS>(a.row_context[r], a.window).count + kStreamUnitCost : 0);
   }
   total *= U;
-  // The tile sequence is numbered in 32 bits from here on (fewer scalar
-  // registers in the tile loop): the host sends only batches whose tiles,
-  // with row_context <= max_context, stay below 2^31 (stream_tiles_fit). A
+  // The positions are numbered in 32 bits from here on (fewer scalar
+  // registers in the tile loop): the host sends only batches whose positions,
+  // with row_context <= max_context, stay below the limit (stream_tiles_fit). A
   // caller whose row_context exceeds its max_context can still get here; then
   // every output row becomes NaN and every span record is marked unwritten,
   // so the merge leaves those rows alone instead of combining stale partials.
-  if (total + sa.wgs >= (int64_t(1) << 31)) {
+  if (total >= stream_position_limit(sa.wgs)) {
     for (int r = w; r < a.rows; r += sa.wgs) {
       const int orow = a.row_map ? a.row_map[r] : r;
       uint16_t* dst = a.out + (int64_t)orow * a.out_stride;

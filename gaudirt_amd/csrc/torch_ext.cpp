@@ -373,7 +373,7 @@ class PagedMetadata : public torch::CustomClassHolder {
         breaks |= static_cast<uint32_t>(p) | static_cast<uint32_t>(s0);
         const int32_t shift = s0 - p;  // slot - position along the run (slots are below 2^31 - 1)
         int32_t q = p + 1;
-        while (q + 8 <= last + 1) {
+        while (int64_t{q} + 8 <= int64_t{last} + 1) {
           bool broken = false;
           for (int k = 0; k < 8; ++k) broken |= row_map[q + k] - (q + k) != shift;
           if (broken) break;

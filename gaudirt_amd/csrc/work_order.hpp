@@ -108,13 +108,15 @@ constexpr StreamStart stream_start(uint32_t off, uint32_t weight, int cost) {
 
 // The balanced schedule numbers the positions of a whole batch (units *
 // (tiles + cost) of each row) in 32 bits, and its kernel splits them over
-// `wgs` workgroups with (total + wgs - 1) / wgs: total + wgs must stay below
-// 2^31. With every row_context <= max_context a row has at most
+// `wgs` workgroups with (total + wgs - 1) / wgs, and a workgroup's cursor
+// steps up to the cost past the last position: total + wgs + cost must stay
+// below 2^31. With every row_context <= max_context a row has at most
 // max_context / ts + 2 tiles, so the host runs the schedule only when this
 // holds.
+constexpr int64_t stream_position_limit(int64_t wgs) { return (int64_t(1) << 31) - wgs - kStreamUnitCost; }
 constexpr bool stream_tiles_fit(int64_t units, int64_t max_context, int ts, int64_t wgs) {
   return units >= 0 && max_context >= 0 && wgs >= 1 &&
-         units * (max_context / ts + 2 + kStreamUnitCost) + wgs < (int64_t(1) << 31);
+         units * (max_context / ts + 2 + kStreamUnitCost) < stream_position_limit(wgs);
 }
 
 }  // namespace gk

@@ -307,9 +307,9 @@ def _stream_grid_workgroups(lib, params):
 def test_stream_routing_boundary_includes_the_grid(runner):
     # Host only (no launch): the balanced schedule numbers a batch's positions
     # (tiles plus a fixed cost per unit) in 32 bits, so gk_paged_decode takes it
-    # exactly while units * (max_context / 32 + 2 + cost) + workgroups < 2^31,
-    # and the partitioned kernel (a non-zero partition) from there on. The
-    # rows are chosen so that the workgroup term decides: without it the
+    # exactly while units * (max_context / 32 + 2 + cost) + workgroups + cost
+    # < 2^31, and the partitioned kernel (a non-zero partition) from there on.
+    # The rows are chosen so that the workgroup term decides: without it the
     # boundary would lie one tile per row later.
     import ctypes
     from gaudirt_amd import capi
@@ -329,15 +329,16 @@ def test_stream_routing_boundary_includes_the_grid(runner):
     print("balanced grid workgroups", wgs, flush=True)
     limit = 1 << 31
     checked = 0
+    cost = capi.STREAM_UNIT_COST
+    fixed = 2 + cost  # per-row position bound n = max_context / 32 + fixed
     for rows in range(65535, 0, -1):
         units = rows * 8
-        n = (limit - 1) // units  # largest tile bound without the grid term
-        if units * n + wgs < limit or n < 3:
+        n = (limit - 1) // units  # largest position bound without the grid term
+        if units * n + wgs + cost < limit or n < fixed + 1:
             continue  # the grid term does not decide for this batch
         params.rows = rows
-        fixed = 2 + capi.STREAM_UNIT_COST  # per-row bound n = max_context / 32 + fixed
         params.max_context = (n - fixed) * 32 - 1  # bound n - 1: fits with the grid term
-        assert units * (n - 1) + wgs < limit
+        assert units * (n - 1) + wgs + cost < limit
         assert lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0, (rows, params.max_context)
         params.max_context = (n - fixed) * 32  # bound n: fits only without the grid term
         assert lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) != 0, (rows, params.max_context)

@@ -123,6 +123,17 @@ def test_paged_attention_two_layers(torch_ext, geometry, rows):
             torch.ops.gaudirt.paged_attn.default(q, k, v, key_pool, value_pool, meta, 96, scale)
 
 
+def test_paged_attention_at_the_row_limit(torch_ext):
+    # 8192 rows, the reference's largest metadata (kMaxRows,
+    # src/bridge/paged_metadata.hpp:19; one more is rejected on the CPU): 128
+    # requests with 64 interleaved decode rows each, store and attention
+    # checked against the oracle.
+    torch = torch_ext
+    results, _, _ = run_case(torch, 4, 2, 64, 128, 128, 8192)
+    for actual, problem, _, _ in results:
+        print("rows 8192 max/mean abs", check(actual, problem), flush=True)
+
+
 def test_repeat_is_deterministic(torch_ext):
     torch = torch_ext
     a, _, _ = run_case(torch, 56, 8, 128, 64, 32, 137)

@@ -113,8 +113,8 @@ void check_stream_gate() {
   for (int ts : {16, 32}) {
     for (int64_t wgs : {int64_t(1), int64_t(256), int64_t(1024), int64_t(4096)}) {
       for (int64_t units : {int64_t(1), int64_t(7), int64_t(1023), int64_t(65535), int64_t(65535) * 8 * 4}) {
-        // The largest per-row tile bound n = max_context / ts + 2 the gate admits.
-        const int64_t n_max = (limit - 1 - wgs) / units;
+        // The largest per-row position bound n = max_context / ts + 2 + cost the gate admits.
+        const int64_t n_max = (gk::stream_position_limit(wgs) - 1) / units;
         const int64_t fixed = 2 + gk::kStreamUnitCost;  // n = max_context / ts + fixed
         if (n_max < fixed) continue;
         const int64_t mc_fit = (n_max - fixed) * ts + ts - 1, mc_over = (n_max - fixed + 1) * ts;
@@ -128,9 +128,10 @@ void check_stream_gate() {
         // Every row at mc_fit under the windows that maximise its tiles.
         for (int window : {0, ts - 1, ts + 1, 2 * ts - 1, (int)std::min<int64_t>(mc_fit, 0x7fffffff)}) {
           const int64_t total = units * (gk::stream_row_tile_count((int)mc_fit, window, ts) + gk::kStreamUnitCost);
-          if (total + wgs >= limit) {
+          // The kernel's own test, and room for its cursor's last step past the end.
+          if (total >= gk::stream_position_limit(wgs) || total + wgs + gk::kStreamUnitCost >= limit) {
             if (failures++ < 10)
-              std::printf("ts=%d wgs=%lld units=%lld window=%d: gate passed but total %lld + wgs reaches 2^31\n", ts,
+              std::printf("ts=%d wgs=%lld units=%lld window=%d: gate passed but total %lld reaches the limit\n", ts,
                           (long long)wgs, (long long)units, window, (long long)total);
             return;
           }
