@@ -41,6 +41,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 namespace gk {
 namespace {
@@ -750,36 +751,42 @@ __global__ __launch_bounds__(64) void stream_merge_kernel(StreamMergeArgs m) {
   if (first_slot < 0 || w_last >= m.wgs) return;  // not a span this call wrote
   const int nslots = w_last - w_first + 1;
   auto slot_of_part = [&](int k) { return k == 0 ? first_slot : 2 * (w_first + k); };
-  // One pass with a running max; the partials of four slots are loaded
-  // together, so a unit costs about one memory round trip per four slots.
-  constexpr int BATCH = 4;
+  // One pass with a running max; the partials of BATCH slots are loaded
+  // together, one memory round trip per batch: batches of four for units of
+  // up to four parts, of sixteen for longer units (long contexts spread one
+  // unit over many workgroups).
   float mm = -INFINITY, ll = 0.f;
   float acc[PER_LANE];
 #pragma unroll
   for (int e = 0; e < PER_LANE; ++e) acc[e] = 0.f;
-  for (int k0 = 0; k0 < nslots; k0 += BATCH) {
-    float mp[BATCH], lp[BATCH], op[BATCH][PER_LANE];
+  auto merge_parts = [&](auto batch) {
+    constexpr int BATCH = decltype(batch)::value;
+    for (int k0 = 0; k0 < nslots; k0 += BATCH) {
+      float mp[BATCH], lp[BATCH], op[BATCH][PER_LANE];
 #pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      const int64_t pi = (int64_t)slot_of_part(min(k0 + u, nslots - 1)) * m.heads_per_group + hh;
-      mp[u] = m.part_ml[pi * 2];
-      lp[u] = m.part_ml[pi * 2 + 1];
+      for (int u = 0; u < BATCH; ++u) {
+        const int64_t pi = (int64_t)slot_of_part(min(k0 + u, nslots - 1)) * m.heads_per_group + hh;
+        mp[u] = m.part_ml[pi * 2];
+        lp[u] = m.part_ml[pi * 2 + 1];
 #pragma unroll
-      for (int e = 0; e < PER_LANE; ++e) op[u][e] = m.part_o[pi * D + lane + 64 * e];
+        for (int e = 0; e < PER_LANE; ++e) op[u][e] = m.part_o[pi * D + lane + 64 * e];
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        // Slots past the unit's last (clamped duplicates) weigh zero.
+        const float mu = k0 + u < nslots ? mp[u] : -INFINITY;
+        const float mn = fmaxf(mm, mu);
+        const float fa = mm == -INFINITY ? 0.f : fast_exp2(mm - mn);
+        const float fb = mu == -INFINITY ? 0.f : fast_exp2(mu - mn);
+        ll = ll * fa + lp[u] * fb;
+#pragma unroll
+        for (int e = 0; e < PER_LANE; ++e) acc[e] = acc[e] * fa + op[u][e] * fb;
+        mm = mn;
+      }
     }
-#pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      // Slots past the unit's last (clamped duplicates) weigh zero.
-      const float mu = k0 + u < nslots ? mp[u] : -INFINITY;
-      const float mn = fmaxf(mm, mu);
-      const float fa = mm == -INFINITY ? 0.f : fast_exp2(mm - mn);
-      const float fb = mu == -INFINITY ? 0.f : fast_exp2(mu - mn);
-      ll = ll * fa + lp[u] * fb;
-#pragma unroll
-      for (int e = 0; e < PER_LANE; ++e) acc[e] = acc[e] * fa + op[u][e] * fb;
-      mm = mn;
-    }
-  }
+  };
+  if (nslots <= 4) merge_parts(std::integral_constant<int, 4>{});
+  else merge_parts(std::integral_constant<int, 16>{});
   const float inv = ll > 0.f ? 1.f / ll : 0.f;
   const int orow = m.row_map ? m.row_map[row] : row;
   uint16_t* dst = m.out + (int64_t)orow * m.out_stride + (int64_t)head * D;
