@@ -669,3 +669,101 @@ def test_slot_allocator_random_against_oracle(torch_ext):
         ext._allocate_paged_slots(torch.tensor([-1]).cuda(), torch.tensor([5]).cuda(), [0], [33], 16)
     with pytest.raises(RuntimeError, match="invalid request lengths"):
         ext._allocate_paged_slots(torch.tensor([-1]).cuda(), torch.tensor([5]).cuda(), [-1], [3], 16)
+
+
+def test_metadata_of_every_constructor_on_two_streams(torch_ext):
+    """tests/paged_metadata_event_reuse_smoke.py and
+    tests/paged_staging_event_lifetime_smoke.py of the reference: metadata from
+    the host constructor, _from_scheduler, from_device_with_tokens and
+    _from_scheduler_fused, built on two streams in turn for 24 rounds and all
+    kept alive, then released in reverse order and built again. Every object
+    keeps its own rows, positions and tokens, and attention through it on its
+    stream is bit-identical across constructors and within the gate of the
+    oracle. (The reference also counts its runtime's events; here the torch
+    caching allocators own device and pinned staging memory.)"""
+    import gaudirt_amd
+
+    torch = torch_ext
+    mapping = torch.arange(1, 129, dtype=torch.int32).reshape(2, 64)
+    d_mapping = mapping.cuda()
+    slots, heads, kv_heads, dim = 129, 4, 2, 128
+    scale = float(np.float32(1.0 / math.sqrt(dim)))
+    gen = torch.Generator().manual_seed(4404)
+    pool = gaudirt_amd.allocate_paged_kv(1, slots, kv_heads, dim)
+    key_pool, value_pool = gaudirt_amd.kv_pool_views(pool, 0)
+    key_pool.copy_(torch.randn(slots, kv_heads, dim, generator=gen).to(torch.bfloat16))
+    value_pool.copy_(torch.randn(slots, kv_heads, dim, generator=gen).to(torch.bfloat16))
+    cases = []
+    for request, prefix in ((0, 5), (1, 12)):
+        positions = torch.arange(prefix, prefix + 3, dtype=torch.int64)
+        requests = torch.full((3,), request, dtype=torch.int64)
+        locations = mapping[requests, positions].long()
+        tokens = torch.tensor([11, 12, 13], dtype=torch.int64) + 100 * request
+        query = torch.randn(3, heads * dim, generator=gen).to(torch.bfloat16)
+        cases.append(dict(request=request, prefix=prefix, positions=positions, requests=requests,
+                          locations=locations, tokens=tokens, query=query.cuda(),
+                          device=[t.cuda() for t in (locations, torch.tensor([request]), positions, tokens)]))
+
+    def construct(case, mode):
+        loc, breq, pos, tok = case["device"]
+        if mode == "host":
+            return torch.classes.gaudirt.PagedMetadata(case["locations"], case["requests"], case["positions"],
+                                                       mapping, slots)
+        if mode == "scheduler":
+            return torch.classes.gaudirt.PagedMetadata._from_scheduler(loc, breq, pos, d_mapping, [case["prefix"]],
+                                                                       [3], slots, tok, 32000)
+        if mode == "checked":
+            return torch.classes.gaudirt.PagedMetadata.from_device_with_tokens(
+                loc, breq, pos, d_mapping, [case["prefix"]], [3], slots, tok, 32000)
+        return torch.classes.gaudirt.PagedMetadata._from_scheduler_fused(
+            loc, breq, case["positions"], d_mapping, [case["prefix"]], [3], slots, tok, 32000, heads, kv_heads, dim)
+
+    modes = ("host", "scheduler", "checked", "fused")
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    # The attention step stores each row's own K/V (the pool's values at its
+    # slots), so every step leaves the pool as it was.
+    kv = [(key_pool[c["locations"].cuda()].reshape(3, -1).clone(),
+           value_pool[c["locations"].cuda()].reshape(3, -1).clone()) for c in cases]
+    torch.cuda.synchronize()
+
+    def build(rounds):
+        pending = []
+        for it in range(rounds):
+            index = it % 2
+            with torch.cuda.stream(streams[index]):
+                for mode in modes:
+                    meta = construct(cases[index], mode)
+                    out = torch.ops.gaudirt.paged_attn.default(cases[index]["query"], kv[index][0], kv[index][1],
+                                                               key_pool, value_pool, meta, dim, scale)
+                    pending.append((index, mode, meta, out))
+        return pending
+
+    def verify(pending):
+        torch.cuda.synchronize()
+        first = {}
+        for index, mode, meta, out in pending:
+            case = cases[index]
+            assert meta.row_locations().cpu().tolist() == case["locations"].tolist(), (index, mode)
+            assert meta.rotary_positions().cpu().tolist() == case["positions"].tolist(), (index, mode)
+            if mode != "host":  # device constructors only (batched metadata)
+                assert meta.last_token_indices().cpu().tolist() == [2], (index, mode)
+                assert meta.token_ids().cpu().tolist() == case["tokens"].tolist(), (index, mode)
+            got = bits(out)
+            if index not in first:
+                first[index] = got
+                problem = orc.Problem(bits(case["query"]), np.stack([bits(key_pool.transpose(0, 1)),
+                                                                     bits(value_pool.transpose(0, 1))]),
+                                      case["requests"].numpy(), case["positions"].numpy(), mapping.numpy(),
+                                      heads, kv_heads, dim, scale)
+                orc.check_flat_gate(got, orc.direct_bf16_pv(problem))
+            assert np.array_equal(got, first[index]), (index, mode)
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    pending = build(24)
+    verify(pending)
+    while pending:
+        pending.pop()
+    pending = build(16)
+    verify(pending)
