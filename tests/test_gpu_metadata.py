@@ -767,3 +767,57 @@ def test_metadata_of_every_constructor_on_two_streams(torch_ext):
         pending.pop()
     pending = build(16)
     verify(pending)
+
+
+@pytest.mark.parametrize("slots,context,requests_n", [(7, 6, 1), (129, 64, 2), (1 << 20, 4096, 64)])
+def test_scheduler_metadata_at_any_capacity(torch_ext, slots, context, requests_n):
+    """tests/scheduler_metadata_capacity_cache_smoke.py of the reference:
+    scheduler metadata over a mostly-zero request map of any slot, context and
+    request capacity keeps the caller's device map itself (no copy), reports
+    its rows, tokens and last-token index, and takes locations at the top of
+    the slot range through the same map updated in place. (The reference also
+    checks that its compiled recipe does not depend on the capacities.)"""
+    torch = torch_ext
+    mapping = torch.zeros((requests_n, context), dtype=torch.int32)
+    mapping[0, :6] = torch.arange(1, 7, dtype=torch.int32)
+    locations = torch.tensor([4, 5, 6], dtype=torch.int64)
+    request = torch.tensor([0], dtype=torch.int64)
+    positions = torch.tensor([3, 4, 5], dtype=torch.int64)
+    tokens = torch.tensor([21, 22, 23], dtype=torch.int64)
+    mapping_device = mapping.cuda()
+    device = [value.cuda() for value in (locations, request, positions, tokens)]
+    metadata = torch.classes.gaudirt.PagedMetadata._from_scheduler(
+        device[0], device[1], device[2], mapping_device, [3], [3], slots, device[3], 32000)
+    actual = [metadata.row_locations().cpu(), metadata.row_requests().cpu(), metadata.rotary_positions().cpu(),
+              metadata.token_ids().cpu(), metadata.last_token_indices().cpu()]
+    expected = [locations.int(), torch.zeros(3, dtype=torch.int32), positions.int(), tokens.int(),
+                torch.tensor([2], dtype=torch.int32)]
+    assert all(torch.equal(a, b) for a, b in zip(actual, expected))
+    assert metadata.slots() == slots and metadata.context() == context
+    assert metadata.request_mapping().data_ptr() == mapping_device.data_ptr()
+    high_locations = torch.arange(slots - 3, slots, dtype=torch.int64)
+    mapping_device[0, 3:6].copy_(high_locations.int())
+    high = torch.classes.gaudirt.PagedMetadata._from_scheduler(
+        high_locations.cuda(), device[1], device[2], mapping_device, [3], [3], slots, device[3], 32000)
+    assert torch.equal(high.row_locations().cpu(), high_locations.int())
+    # and attention through it reads the top slots (store, then decode rows 3..5 over keys 0..5)
+    import gaudirt_amd
+
+    heads, kv_heads, dim = 4, 2, 64
+    gen = torch.Generator().manual_seed(slots % 1000)
+    pool = gaudirt_amd.allocate_paged_kv(1, slots, kv_heads, dim)
+    key_pool, value_pool = gaudirt_amd.kv_pool_views(pool, 0)
+    key_pool.copy_(torch.randn(slots, kv_heads, dim, generator=gen).to(torch.bfloat16))
+    value_pool.copy_(torch.randn(slots, kv_heads, dim, generator=gen).to(torch.bfloat16))
+    q = torch.randn(3, heads * dim, generator=gen).to(torch.bfloat16)
+    k = torch.randn(3, kv_heads * dim, generator=gen).to(torch.bfloat16)
+    v = torch.randn(3, kv_heads * dim, generator=gen).to(torch.bfloat16)
+    scale = float(np.float32(1.0 / math.sqrt(dim)))
+    out = torch.ops.gaudirt.paged_attn.default(q.cuda(), k.cuda(), v.cuda(), key_pool, value_pool, high, dim, scale)
+    torch.cuda.synchronize()
+    bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)  # noqa: E731
+    pool_bits = np.stack([bits(key_pool.transpose(0, 1)), bits(value_pool.transpose(0, 1))])
+    assert np.array_equal(pool_bits[0][:, slots - 3:], bits(k.reshape(3, kv_heads, dim).transpose(0, 1)))
+    problem = orc.Problem(bits(q), pool_bits, np.zeros(3, dtype=np.int64), positions.numpy(),
+                          mapping_device.cpu().numpy(), heads, kv_heads, dim, scale)
+    orc.check_flat_gate(bits(out), orc.direct_bf16_pv(problem))
