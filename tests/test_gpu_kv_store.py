@@ -60,6 +60,33 @@ def test_tile_indices_bit_exact(runner):
     assert np.array_equal(out.cpu().numpy().reshape(500, 64), expected)
 
 
+@pytest.mark.parametrize("requests_n,context,slots", [(2, 73, 2), (7, 1000, 4097), (256, 131072, 131072)])
+def test_tile_indices_reference_device_cases(runner, requests_n, context, slots):
+    # tests/attention_tile_indices_device_test.cpp of the reference, its own
+    # construction and closed-form expectation (no oracle): map[r][i] = 1 +
+    # (11 r + 7 i) mod (slots - 1); eight tasks alternating row 0 (request 0,
+    # keys 0.., 64 lanes) and row 1 (the last request, keys 64.., 9 lanes),
+    # base (t / 2) * slots; every one of the 64 lanes written.
+    import torch
+    from gaudirt_amd import capi
+    r = np.arange(requests_n)[:, None]
+    i = np.arange(context)[None, :]
+    mapping = (1 + (r * 11 + i * 7) % (slots - 1)).astype(np.int32)
+    row_requests = np.array([0, requests_n - 1], dtype=np.int32)
+    tasks = 8
+    work = np.array([[t % 2, (t % 2) * 64, 9 if t % 2 else 64, (t // 2) * slots] for t in range(tasks)],
+                    dtype=np.int32)
+    out = torch.full((tasks * 64,), -123, dtype=torch.int32, device="cuda")
+    d_map, d_req, d_work = (runner.to_device(a) for a in (mapping, row_requests, work))
+    capi.check(capi.load().gk_attn_tile_indices(capi.ptr(d_map), capi.ptr(d_req), capi.ptr(d_work), tasks, context,
+                                                capi.ptr(out), capi.current_stream()))
+    got = out.cpu().numpy().reshape(tasks, 64)
+    for t in range(tasks):
+        req, first, lanes, base = row_requests[work[t, 0]], work[t, 1], work[t, 2], work[t, 3]
+        want = [base + (mapping[req, first + lane] if lane < lanes else 0) for lane in range(64)]
+        assert got[t].tolist() == want, t
+
+
 @pytest.mark.parametrize("count", [1, 3, 16, 70000])
 def test_advance_decode_lengths(runner, count):
     import torch
