@@ -21,7 +21,7 @@ of its own (a pool allocated after others were released ran ~4% slower); the
 CPU baseline runs last.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20 (c4: 1000)] [--workload c2] [--no-cpu]
-                    [--no-secondary] [--host-overhead]
+                    [--no-secondary] [--host-overhead] [--page-size N]
 
 --host-overhead instead times the drop-in op torch.ops.gaudirt.paged_attn on
 C2's decode step (store of each row's new K/V, then attention), host side and
@@ -74,6 +74,9 @@ def parse_args():
     ap.add_argument("--table-sets", type=int, default=3)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = library choice)")
+    ap.add_argument("--page-size", type=int, default=0,
+                    help="decode workloads: re-page the block tables to pages of this many tokens (same tokens; "
+                         "1 = the token-granular map); 0 = the workload's block size")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true",
                     help="headline workload only (no c3/c4/c5 entries after a c2 headline)")
@@ -233,10 +236,11 @@ def prefill_bench(args):
         "roofline": prefill_roofline(tflops), "cpu_baseline": None}), flush=True)
 
 
-def decode_run(lib, workload, steps, warmup, table_sets, seed, partition):
+def decode_run(lib, workload, steps, warmup, table_sets, seed, partition, page_size=0):
     """One gk_paged_decode call per step over the whole batch of a decode workload,
     timed with HIP events on the launch stream; consecutive steps rotate over
-    `table_sets` disjoint block-table sets. Returns a dict of the timing and the case."""
+    `table_sets` disjoint block-table sets (re-paged to `page_size` tokens per
+    page when given). Returns a dict of the timing and the case."""
     import torch
 
     from gaudirt_amd import capi, workloads
@@ -244,13 +248,18 @@ def decode_run(lib, workload, steps, warmup, table_sets, seed, partition):
     dc = workloads.DeviceDecodeCase(workload, seed=seed, table_sets=table_sets)
     stream = torch.cuda.current_stream()
     hstream = ctypes.c_void_p(stream.cuda_stream)
+    page = page_size or dc.block_size
+    table_sets_dev = dc.d_table_sets
+    if page != dc.block_size:
+        table_sets_dev = [torch.from_numpy(workloads.repage_tables(t, dc.lens, dc.block_size, page)).cuda()
+                          for t in dc.table_sets]
 
     params = []
-    for i, tables in enumerate(dc.d_table_sets):
+    for i, tables in enumerate(table_sets_dev):
         p = capi.DecodeParams()
         p.query, p.q_row_stride = dc.query.data_ptr(), dc.query.stride(0)
         p.pool, p.slots = dc.pool.data_ptr(), dc.slots
-        p.block_tables, p.bt_stride, p.block_size = tables.data_ptr(), tables.stride(0), dc.block_size
+        p.block_tables, p.bt_stride, p.block_size = tables.data_ptr(), tables.stride(0), page
         p.row_request, p.row_context, p.rows = None, dc.d_lens.data_ptr(), dc.batch
         p.q_heads, p.kv_heads, p.head_dim = dc.heads, dc.kv_heads, dc.head_dim
         p.scale, p.softcap, p.sliding_window = dc.scale, 0.0, -1
@@ -285,7 +294,7 @@ def decode_run(lib, workload, steps, warmup, table_sets, seed, partition):
     ms_per_step = start.elapsed_time(end) / steps
     del workspace
 
-    step_bytes = dc.step_bytes()
+    step_bytes = dc.step_bytes(page)
     kv_bytes = dc.kv_bytes()
     seconds = ms_per_step * 1e-3
     achieved = step_bytes / seconds / 1e9
@@ -298,6 +307,7 @@ def decode_run(lib, workload, steps, warmup, table_sets, seed, partition):
         "ms_per_step": ms_per_step,
         "tokens_per_s": tokens_per_s,
         "partition": int(chosen),
+        "page_size": page,
         "table_sets": len(params),
         "kv_read_gbps": kv_bytes / seconds / 1e9,
         "roofline": {
@@ -306,7 +316,9 @@ def decode_run(lib, workload, steps, warmup, table_sets, seed, partition):
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": measured_traffic(workload, int(chosen)),
+            # the recorded counters are for the workload's own block size (another
+            # page size runs another variant of the kernel)
+            "traffic": measured_traffic(workload, int(chosen)) if page == dc.block_size else None,
         },
     }
 
@@ -456,7 +468,8 @@ def main():
     from gaudirt_amd import capi
 
     lib = capi.load()
-    r = decode_run(lib, args.workload, args.steps, args.warmup, args.table_sets, args.seed, args.partition)
+    r = decode_run(lib, args.workload, args.steps, args.warmup, args.table_sets, args.seed, args.partition,
+                   args.page_size)
     dc = r["case"]
     # The GPU legs run back to back; the CPU baseline (about a second of host
     # work with the GPU idle) comes last.
@@ -487,7 +500,7 @@ def main():
             "q_heads": dc.heads,
             "kv_heads": dc.kv_heads,
             "head_dim": dc.head_dim,
-            "block_size": dc.block_size,
+            "block_size": r["page_size"],
             "mean_context": float(dc.lens.mean()),
             "max_context": int(dc.lens.max()),
             "split_k_partition": r["partition"],

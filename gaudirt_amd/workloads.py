@@ -32,6 +32,19 @@ def permuted_block_tables(rng, lens, block_size, num_blocks, sets=1):
     return tables[0] if sets == 1 else tables
 
 
+def repage_tables(table, lens, block_size, page_size):
+    """The same tokens as `table` (blocks of `block_size` tokens), as a table of
+    pages of `page_size` tokens (a power of two dividing block_size): entry k of
+    row b is the page holding token k * page_size, -1 past the row's length."""
+    assert 0 < page_size <= block_size and block_size % page_size == 0
+    pages = [(int(n) + page_size - 1) // page_size for n in lens]
+    out = np.full((len(lens), max(pages)), -1, dtype=np.int32)
+    for b, n in enumerate(pages):
+        t = np.arange(n, dtype=np.int64) * page_size
+        out[b, :n] = (table[b, t // block_size].astype(np.int64) * block_size + t % block_size) // page_size
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Full-size configurations (generated on the GPU; need torch + a device)
 # ---------------------------------------------------------------------------
@@ -94,12 +107,14 @@ class DeviceDecodeCase:
     def kv_bytes(self):
         return int(self.lens.astype(np.int64).sum()) * self.kv_heads * self.head_dim * 2 * 2
 
-    def step_bytes(self):
+    def step_bytes(self, page_size=None):
         """Algorithmic HBM bytes of one step: K/V rows read, Q read, O written, tables and lengths,
-        plus the store's read and write of the new rows when the case stores."""
+        plus the store's read and write of the new rows when the case stores. `page_size`: the
+        table's page (default the case's block size)."""
+        page = page_size or self.block_size
         b = self.kv_bytes()
         b += 2 * self.batch * self.heads * self.head_dim * 2
-        b += int(((self.lens.astype(np.int64) + self.block_size - 1) // self.block_size).sum()) * 4 + 4 * self.batch
+        b += int(((self.lens.astype(np.int64) + page - 1) // page).sum()) * 4 + 4 * self.batch
         if self.store:
             b += 2 * 2 * self.batch * self.kv_heads * self.head_dim * 2 + 4 * self.batch
         return b

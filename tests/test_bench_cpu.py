@@ -62,3 +62,22 @@ def test_more_than_one_gpu_is_refused():
                           text=True, timeout=120)
     assert proc.returncode == 2
     assert "one GPU" in proc.stderr
+
+
+def test_repaged_tables_hold_the_same_tokens():
+    # bench.py --page-size: a block table re-paged to smaller pages names the
+    # same slot for every token of every row, and nothing past a row's length.
+    import numpy as np
+
+    from gaudirt_amd import workloads
+
+    rng = np.random.default_rng(0)
+    lens = np.array([1, 127, 128, 129, 300, 4096])
+    table = workloads.permuted_block_tables(rng, lens, 128, 64)
+    for page in (128, 64, 16, 4, 2, 1):
+        paged = workloads.repage_tables(table, lens, 128, page)
+        for row, n in enumerate(lens):
+            tokens = np.arange(n)
+            want = table[row, tokens // 128] * 128 + tokens % 128
+            assert np.array_equal(paged[row, tokens // page] * page + tokens % page, want), (page, row)
+            assert (paged[row, (n + page - 1) // page:] == -1).all(), (page, row)
