@@ -33,7 +33,7 @@
 // subset of the HBM channels.
 //
 // The per-tile arithmetic is the partitioned MFMA kernel's (paged_decode.hip):
-// S^T = K . Q^T with v_mfma_f32_16x16x32_bf16, lazy online softmax, P rounded
+// S^T = K . Q^T with v_mfma_f32_16x16x32_bf16, online softmax, P rounded
 // to bf16, P . V from a transposed LDS read, both tiles loaded HBM -> LDS with
 // 16-byte buffer loads (global_load_lds_dwordx4).
 #include "decode_common.hpp"
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   bf16x8_t qb[S::NC];
   f32x4_t o[S::NO];
   float m_run = -INFINITY, l_run = 0.f;
-  // Without softcap: (m_run + kDecodeLazyRescale) / scale, the raw-score
+  // Without softcap: (m_run + kDecodeRescaleSlack) / scale, the raw-score
   // threshold of a re-base; and the base of the probabilities (m_run, or 0
   // before the first maximum). Both change only at a re-base.
   float m_thr = -INFINITY, m_base = 0.f;
@@ -568,7 +568,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
 
     // Mask, and the row maximum over this lane's scores. Without softcap the
     // scores stay raw: a tile whose keys are all visible needs no per-element
-    // mask, the maximum is compared with (m_run + kDecodeLazyRescale) / scale
+    // mask, the maximum is compared with (m_run + kDecodeRescaleSlack) / scale
     // (kept with m_run), and the scale folds into the exponent below.
     const bool inside = !SOFTCAP && t.tb >= t.left && t.tb + TS <= t.ctx;  // wave-uniform
     if (!inside) {
@@ -589,12 +589,12 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       for (int i = 0; i < 4 * S::TG; ++i) v[i] = sc[i >> 2][i & 3];
       mx = col4_max(tree_max(v));
     }
-    if (__builtin_amdgcn_ballot_w64(mx > (SOFTCAP ? m_run + kDecodeLazyRescale : m_thr))) {
+    if (__builtin_amdgcn_ballot_w64(mx > (SOFTCAP ? m_run + kDecodeRescaleSlack : m_thr))) {
       const float m_new = fmaxf(m_run, SOFTCAP ? mx : mx * a.score_scale);
       const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
       l_run *= alpha;
       m_run = m_new;
-      m_thr = (m_new + kDecodeLazyRescale) * inv_scale;
+      m_thr = (m_new + kDecodeRescaleSlack) * inv_scale;
       m_base = m_new == -INFINITY ? 0.f : m_new;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {

@@ -6,7 +6,10 @@
 // partition's block-table entries are staged in LDS first, so no K/V load ever
 // waits on another load (a block-table lookup is an LDS read).
 //
-// Two kernels compute a partition:
+// These kernels run when the caller fixes the partition (a row's output then
+// depends on that row alone) or when a batch exceeds the balanced schedule's
+// 32-bit numbering; otherwise decode_stream.hip's balanced schedule runs. Two
+// kernels compute a partition:
 //
 //  * decode_mfma_kernel (GQA group >= 4, head_dim 64/128/256): one wave per
 //    work item. The group's query heads are the 16 rows of bf16 MFMA tiles.
@@ -20,7 +23,8 @@
 //    [token][dim] of P.V.
 //
 //  * decode_dot_kernel (groups 1..3, where a 16-row MFMA tile would be mostly
-//    padding): a workgroup of four waves per work item. Q.K and P.V run as
+//    padding, which the partitioned grid's short items would pay for): a
+//    workgroup of four waves per work item. Q.K and P.V run as
 //    wave-level bf16 dot2 (v_dot2_f32_bf16) with fp32 accumulation. A head row
 //    of D bf16 is split over LPT = D/16 lanes; one load instruction covers
 //    TPW = 64/LPT consecutive tokens, so every cache line fetched is used in
@@ -228,7 +232,7 @@ __global__ __launch_bounds__(64, mfma_waves_per_simd<D>()) void decode_mfma_kern
         mx = fmaxf(mx, s);
       }
     mx = col4_max(mx);
-    if (__builtin_amdgcn_ballot_w64(mx > m_run + kDecodeLazyRescale)) {
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kDecodeRescaleSlack)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
       l_run *= alpha;
@@ -725,16 +729,17 @@ int device_cus() {
 //  - Otherwise 2048-key items while one round of them (at the expected mean
 //    length max_context / 2) fits the resident waves, else 1024.
 // dot2 path: halve a 2048-key partition until the items fill the GPU.
-// The balanced schedule (decode_stream.hip) serves the MFMA path, every block
-// size included, whenever the caller leaves the partition to the library; an
-// explicit partition and small groups take the partitioned kernels.
+// The balanced schedule (decode_stream.hip) serves every GQA group and block
+// size whenever the caller leaves the partition to the library (at groups 1-3
+// most of its 16 MFMA head columns are padding, which costs nothing against
+// the K/V stream); an explicit partition takes the partitioned kernels.
 // The balanced schedule numbers the batch's tiles in 32 bits: it runs when
 // every row's tiles (at most max_context / TS + 2 with a window's offset)
 // times the units, plus the grid's workgroups, stay below 2^31 (the kernel's
 // own test, stream_tiles_fit); larger batches take the partitioned kernel.
 bool use_stream(const gk_decode_params* p) {
   const int group = p->q_heads / p->kv_heads;
-  if (p->partition_tokens != 0 || !use_mfma(group)) return false;
+  if (p->partition_tokens != 0) return false;
   const int hpw = heads_per_workgroup(group);
   const int64_t units = (int64_t)p->rows * p->kv_heads * ((group + hpw - 1) / hpw);
   const int ts = p->head_dim == 256 ? 16 : 32;

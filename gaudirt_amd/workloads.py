@@ -58,6 +58,8 @@ CONFIGS = {
     # C2's batch, lengths, pool and KV bytes at GQA group 2 (16 q / 8 kv heads):
     # the geometry the wave-level dot-product kernel serves.
     "c2g2": (64, 16, 8, 128, 128, 4096, lambda rng, b: rng.integers(512, 4097, b)),
+    # ... and at group 1 (8 q / 8 kv heads, multi-head attention).
+    "c2g1": (64, 8, 8, 128, 128, 4096, lambda rng, b: rng.integers(512, 4097, b)),
 }
 
 

@@ -100,7 +100,7 @@ def test_poisoned_unused_slots_do_not_propagate(runner):
     check_against_oracle(case, actual)
 
 
-@pytest.mark.parametrize("name", ["c2", "c5"])
+@pytest.mark.parametrize("name", ["c2", "c5", "c2g1", "c2g2"])
 def test_full_size_decode(runner, name):
     import torch
     from gaudirt_amd import workloads

@@ -62,7 +62,9 @@ def test_library_choice_is_the_balanced_schedule(runner):
 
 
 @pytest.mark.parametrize("geometry", [(14, 2, 64), (56, 8, 128), (64, 8, 128), (8, 1, 256), (32, 2, 128),
-                                      (64, 2, 128), (24, 1, 64), (40, 2, 256)])
+                                      (64, 2, 128), (24, 1, 64), (40, 2, 256),
+                                      # GQA groups 1-3: 1-3 of the tile's 16 head columns used
+                                      (8, 8, 128), (2, 2, 64), (16, 8, 64), (9, 3, 128), (3, 1, 256), (4, 2, 256)])
 def test_stream_geometries(runner, geometry):
     heads, kv_heads, d = geometry
     rng = np.random.default_rng(heads * 1000 + kv_heads * 10 + d)
@@ -120,20 +122,22 @@ def test_stream_small_blocks_window_evicted(runner, block):
 
 
 def test_library_choice_small_blocks(runner):
-    # Every block size takes the balanced schedule (partition 0) when the
-    # partition is left to the library and the GQA group is at least 4.
+    # Every block size and GQA group takes the balanced schedule (partition 0)
+    # when the partition is left to the library.
     import ctypes
     import torch
     from gaudirt_amd import capi
 
     lib = capi.load()
-    for d, block, heads in [(128, 1, 16), (128, 2, 16), (64, 4, 16), (256, 1, 16), (128, 1, 6)]:
+    for d, block, heads in [(128, 1, 16), (128, 2, 16), (64, 4, 16), (256, 1, 16), (128, 1, 6), (64, 16, 2),
+                            (256, 128, 4)]:
         case = cases.decode_case(1, 2, heads, 2, d, block, 256, [30, 60])
         params = runner.decode_params(runner.bf16_device(case.query), runner.bf16_device(case.pool),
                                       runner.to_device(case.block_tables), runner.to_device(case.lens), heads, 2, d,
                                       block, case.scale, torch.empty(2, heads * d, dtype=torch.bfloat16, device="cuda"))
-        stream = heads // 2 >= 4
-        assert (lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0) == stream, (d, block, heads)
+        assert lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 0, (d, block, heads)
+        params.partition_tokens = 512
+        assert lib.gk_paged_decode_partition_tokens(ctypes.byref(params)) == 512, (d, block, heads)
 
 
 def test_one_long_row_split_over_the_grid(runner):
