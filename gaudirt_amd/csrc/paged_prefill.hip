@@ -107,6 +107,17 @@ constexpr int kStepBlocks = 0, kLoadBlocks = 1, kKeyBlocks = 2;
 #ifndef GK_PREFILL_LAG
 #define GK_PREFILL_LAG 0
 #endif
+// Head_dim 128 software pipeline (build variant, no softcap): iteration i
+// runs Q.K(i) interleaved with the probabilities of step i - 1, then
+// P.V(i - 1) interleaved with the row maxima of step i, so each wave's own
+// instruction stream alternates MFMAs with independent VALU work. V lags K by
+// one step in LDS (the same two K and two V stages).
+#ifndef GK_PREFILL_PIPE
+#define GK_PREFILL_PIPE 0
+#endif
+#ifndef GK_PREFILL_PIPE_ORDER
+#define GK_PREFILL_PIPE_ORDER 1
+#endif
 
 template <int D, bool SOFTCAP, int MODE>
 __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
@@ -131,6 +142,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // starts its output as soon as its own last step ends, with no barrier
   // (132 KiB at head_dim 128, one workgroup per CU either way).
   constexpr bool kLag = GK_PREFILL_LAG && D >= 128 && !SOFTCAP;  // softcap: no registers to spare
+  constexpr bool kPipe = GK_PREFILL_PIPE && D >= 128 && !SOFTCAP && !kLag;
   constexpr int kOutRowBytes = 2 * D + 16;
   constexpr int kKvBytes = (kLag ? 5 : kStages * 2) * S::TILE,
                 kOutBytes = kPrefillWaves * kQrowsPerWave * kOutRowBytes;
@@ -543,6 +555,195 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
       run(std::false_type{});
       // P.V of the last step (its V stage is never refilled).
       accumulate(vstages + (vs == 0 ? 2 : vs - 1) * S::TILE, nullptr);
+    }
+  } else if constexpr (kPipe) {
+    // Iteration i (0 <= i <= nsteps), after the step's barrier:
+    //   loads  K(i + 1) -> K stage (i + 1) % 2 and V(i) -> V stage i % 2 (both
+    //          last read in iteration i - 1);
+    //   A      S(i) = K(i) . Q^T, interleaved with P(i - 1) = exp2(S(i - 1)
+    //          scale - base) (independent instructions of one wave);
+    //   mask   S(i), on steps that cross the diagonal or the window;
+    //   B      O += P(i - 1) . V(i - 1), interleaved with the row maxima of S(i);
+    //   re-base (rare) after B, so P(i - 1) keeps the base it was formed
+    //          against and P(i) is formed against the new one.
+    // The same operations on o and l_run in the same order as the loop below.
+    f32x4_t sp[2][kKG][kNT];
+    Offsets off_v = offsets_of(kb0, entry_of(kb0));  // offsets of the step whose V is issued next
+    issue(off_v, krs, kv[0][0]);
+    Entries e_next{};
+    if (1 < nsteps) e_next = entry_of(kb0 + kKeys);
+
+    auto qk = [&](const char* kt, f32x4_t(&dst)[kKG][kNT]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int h = 0; h < kKG; ++h) {
+        const int tt = 16 * h + c16;
+        bf16x8_t kr[S::NC];
+#pragma unroll
+        for (int c = 0; c < S::NC; ++c)
+          kr[c] = *reinterpret_cast<const bf16x8_t*>(kt + tt * (2 * D) + (((4 * c + q) ^ swz(tt, D / 8)) << 4));
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+          dst[h][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < S::NC; ++c) dst[h][nt] = mfma32(kr[c], qb[nt][c], dst[h][nt]);
+        }
+      }
+    };
+    auto probs = [&](const f32x4_t(&src)[kKG][kNT]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4 * kKG; ++i)
+          pa[i >> 3][nt][i & 7] = (__bf16)fast_exp2(__builtin_fmaf(src[i >> 2][nt][i & 3], a.score_scale, -m_base[nt]));
+    };
+    auto mask = [&](int tb, f32x4_t(&s)[kKG][kNT]) __attribute__((always_inline)) {
+      const bool full = tb + kKeys - 1 <= wave_pos_min && tb >= wave_left_max;
+      if (!full) {
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int h = 0; h < kKG; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = tb + 16 * h + 4 * q + r;
+              s[h][nt][r] = (key <= qpos[nt] && key >= qleft[nt]) ? s[h][nt][r] : -INFINITY;
+            }
+      }
+    };
+    auto row_max = [&](const f32x4_t(&s)[kKG][kNT], float(&mx)[kNT]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        float t[4 * kKG];
+#pragma unroll
+        for (int i = 0; i < 4 * kKG; ++i) t[i] = s[i >> 2][nt][i & 3];
+        mx[nt] = tree_max(t);
+      }
+      static_assert(kNT == 2, "one pair of tiles");
+      col4_max2(mx[0], mx[1]);
+    };
+    auto rebase = [&](const float(&mx)[kNT]) __attribute__((always_inline)) {
+      bool any = false;
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) any = any || mx[nt] > m_thr[nt];
+      if (!__builtin_amdgcn_ballot_w64(any)) return;
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        if (!__builtin_amdgcn_ballot_w64(mx[nt] > m_thr[nt])) continue;
+        const float m_new = fmaxf(m_run[nt], mx[nt] * a.score_scale);
+        const float alpha = m_run[nt] == -INFINITY ? 0.f : fast_exp2(m_run[nt] - m_new);
+        m_run[nt] = m_new;
+        m_thr[nt] = (m_new + kLazyRescale) * inv_scale;
+        m_base[nt] = m_new == -INFINITY ? 0.f : m_new;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float f = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(alpha)));
+#pragma unroll
+          for (int c = 0; c < S::NO; ++c) o[nt][c][r] *= f;
+          l_run[nt][r] *= f;
+        }
+      }
+    };
+    // Barrier and loads of iteration i.
+    auto top = [&](int i, auto stage) __attribute__((always_inline)) {
+      constexpr int cur = decltype(stage)::value, next = cur ^ 1;
+      const int tb = kb0 + i * kKeys;
+      wait_vmem<0>();
+      __syncthreads();
+      wait_vmem_visible();  // as in the loop below
+      if (i + 1 < nsteps) {
+        const Offsets of = offsets_of(tb + kKeys, e_next);
+        issue(of, krs, kv[next][0]);
+        issue(off_v, vrs, kv[cur][1]);
+        off_v = of;
+        if (i + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
+      } else if (i < nsteps) {
+        issue(off_v, vrs, kv[cur][1]);
+      }
+    };
+    // Instruction order of the two phases: one MFMA, then independent VALU
+    // work, with each group's LDS operand reads issued a group ahead.
+    auto order_a = [&]() __attribute__((always_inline)) {
+#if GK_PREFILL_PIPE_ORDER
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int h = 0; h < kKG; ++h) {
+#pragma unroll
+        for (int k = 0; k < 2 * kNT; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x402, 3, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);
+        }
+        if (h + 2 < kKG) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      }
+#endif
+    };
+    auto order_b = [&]() __attribute__((always_inline)) {
+#if GK_PREFILL_PIPE_ORDER
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+#pragma unroll
+      for (int c = 0; c < S::NO; ++c) {
+#pragma unroll
+        for (int k = 0; k < 2 * kNT; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x402, 1, 1);
+        }
+        if (c + 2 < S::NO) __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kNT * kKH, 1);
+#endif
+    };
+    // Empty asm uses of the probabilities at the end of phase A: the compiler
+    // would otherwise sink their computation to P.V, past the mask branch.
+    auto anchor_pa = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int hh = 0; hh < kKH; ++hh)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+          const auto w = __builtin_bit_cast(u32x4_t, pa[hh][nt]);
+          asm volatile("" ::"v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]));
+        }
+    };
+    auto steady = [&](int i, auto stage) __attribute__((always_inline)) {
+      constexpr int cur = decltype(stage)::value, prev = cur ^ 1;
+      top(i, stage);
+      qk(kv[cur][0], sp[cur]);
+      probs(sp[prev]);
+      order_a();
+      anchor_pa();
+      mask(kb0 + i * kKeys, sp[cur]);
+      float mx[kNT];
+      row_max(sp[cur], mx);
+      accumulate(kv[prev][1], nullptr);
+      order_b();
+      rebase(mx);
+    };
+    auto last = [&](int i, auto stage) __attribute__((always_inline)) {
+      constexpr int prev = decltype(stage)::value ^ 1;
+      top(i, stage);
+      probs(sp[prev]);
+      accumulate(kv[prev][1], nullptr);
+    };
+    using Zero = std::integral_constant<int, 0>;
+    using One = std::integral_constant<int, 1>;
+    {
+      top(0, Zero{});
+      qk(kv[0][0], sp[0]);
+      mask(kb0, sp[0]);
+      float mx[kNT];
+      row_max(sp[0], mx);
+      rebase(mx);
+    }
+    int i = 1;
+    for (; i + 1 < nsteps; i += 2) {
+      steady(i, One{});
+      steady(i + 1, Zero{});
+    }
+    if (i < nsteps) {
+      steady(i, One{});
+      last(i + 1, Zero{});
+    } else {
+      last(i, One{});
     }
   } else if constexpr (!kPingPong) {
     // One barrier per step: before it each wave waits for its own loads of
