@@ -60,6 +60,8 @@ WORKLOADS = {
             "4096-block bf16 pool",
     "c2g1": "c2 at GQA group 1: batch 64, 8 q / 8 kv heads, head_dim 128, block 128, ctx U[512,4096], "
             "4096-block bf16 pool",
+    "c2g3": "c2 at GQA group 3: batch 64, 24 q / 8 kv heads, head_dim 128, block 128, ctx U[512,4096], "
+            "4096-block bf16 pool",
 }
 C4_WARMUP = 1000
 MFMA_BF16_PEAK_TFLOPS = 2500.0

@@ -47,6 +47,7 @@ namespace gk {
 namespace {
 
 typedef __attribute__((address_space(3))) char lds_char_t;
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 
 
 struct StreamArgs {
@@ -133,13 +134,39 @@ struct TileEntries {
 // All entries are scalar loads issued one tile ahead.
 constexpr int kTileBlocks = 0, kLoadBlocks = 1, kKeyBlocks = 2;
 
-template <int D, bool SOFTCAP, int MODE>
-__global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
+// Per-tile arithmetic (the ARITH template argument):
+//  kArithMfma  S^T = K . Q^T and P . V on 16 x 16 MFMA tiles whose 16 columns
+//              are a unit's query heads (every GQA group; 1-3 heads leave
+//              padding columns);
+//  kArithDot   groups of 1-3 heads, head_dim 64/128: wave-level v_dot2_f32_bf16
+//              with fp32 accumulation. Q.K: each lane holds one key of the
+//              tile and half of its dims (lanes l and l + 32 the two halves),
+//              the halves added across the 32-lane swap. P.V: each lane owns
+//              D / 64 output dims and reads them for four keys at a time with
+//              the transposed LDS read; the probabilities of two keys at a
+//              time reach every lane as one scalar (a packed bf16 pair).
+// The shipping build runs the MFMA form at every group: under the balanced
+// schedule the dot form measured slower at groups 1, 2 and 3 (same box, C2's
+// batch at 8 / 16 / 24 query heads: 102.0 / 102.5 / 102.9 us against 107.9 /
+// 113.0 / 120.0 us). GK_STREAM_DOT=1 builds the dot form for units of 1-3
+// heads (head_dim 64/128).
+#ifndef GK_STREAM_DOT
+#define GK_STREAM_DOT 0
+#endif
+constexpr int kArithMfma = 0, kArithDot = 1;
+constexpr int kDotMaxHeads = 3;
+
+template <int D, bool SOFTCAP, int MODE, int ARITH>
+__device__ __forceinline__ void decode_stream_body(StreamArgs sa) {
   using S = MfmaShape<D>;
   constexpr int TS = S::TS;
+  constexpr bool DOT = ARITH == kArithDot;
+  static_assert(!DOT || TS == 32, "the dot form pairs each key with two lanes (head_dim 64/128)");
+  constexpr int DNC = D / 16;  // dot form: 16-byte chunks of a key row per lane (half the row)
+  constexpr int DOD = D / 64;  // dot form: output dims per lane
   constexpr int NR = MODE == kTileBlocks ? 1 : MODE == kLoadBlocks ? S::LOADS : TS;  // key runs of a tile
   constexpr int KPR = TS / NR;  // keys of one run
-  constexpr int KPL = 64 / S::CPR;  // keys of one load instruction
+  [[maybe_unused]] constexpr int KPL = 64 / S::CPR;  // keys of one load instruction
   // kKeyBlocks hands its per-key entries straight from the prefetch to the
   // loads (a descriptor holding TS offsets would live in scratch memory).
   using TileDesc = gk::TileDesc<MODE == kKeyBlocks ? 1 : NR>;
@@ -419,12 +446,33 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   bf16x8_t qb[S::NC];
   f32x4_t o[S::NO];
   float m_run = -INFINITY, l_run = 0.f;
+  // Dot form: per head (uniform) running max, threshold and base; per lane
+  // the partial sum of its key's probabilities and its output dims.
+  u32x4_t qd[kDotMaxHeads][DOT ? DNC : 1];
+  float od[kDotMaxHeads][DOT ? DOD : 1];
+  float dm_run[kDotMaxHeads], dm_thr[kDotMaxHeads], dm_base[kDotMaxHeads], dl[kDotMaxHeads];
   // Without softcap: (m_run + kDecodeRescaleSlack) / scale, the raw-score
   // threshold of a re-base; and the base of the probabilities (m_run, or 0
   // before the first maximum). Both change only at a re-base.
   float m_thr = -INFINITY, m_base = 0.f;
   const float inv_scale = 1.f / a.score_scale;
 
+  // Maximum and sum over the 32 keys of a tile in the dot form (lanes l and
+  // l + 32 hold the same key): a 16-lane butterfly, then the two 16-lane rows
+  // of each half combined; every lane receives the result.
+  auto key32_max = [&](float x) {
+    x = max2(x, dpp<kDppQuadXor1>(x));
+    x = max2(x, dpp<kDppQuadXor2>(x));
+    x = max2(x, dpp<kDppRowHalfMirror>(x));
+    x = max2(x, dpp<kDppRowMirror>(x));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return max2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  };
+  auto key32_sum = [&](float x) {
+    x = group_sum<16>(x);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  };
   // Finished segments are not stored right away. The pipeline's waits count
   // every vector memory operation older than the newest tile (vmcnt), so a
   // store issued among the tile loads holds up the next wait until it is
@@ -450,18 +498,33 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
     const bool out = (e.kind & 32) != 0;
     const int head0 = e.kind >> 6;
     const int64_t part = (int64_t)e.dst * a.heads_per_group;  // partial slot's first head
+    if constexpr (DOT) {
+      // Lane (g = lane / 16, i = lane % 16) holds dims DOD * 16 g + 16 j + i
+      // of every head (v[h][j]).
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * q + r;
-      if (h >= hv) continue;
-      if (out) {
-        uint16_t* dst = a.out + (int64_t)e.dst * a.out_stride + (int64_t)(head0 + h) * D + c16;
+      for (int h = 0; h < kDotMaxHeads; ++h) {
+        if (h >= hv) continue;
 #pragma unroll
-        for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(e.v[c][r]);
-      } else {
-        float* dst = a.part_o + (part + h) * D + c16;
+        for (int j = 0; j < DOD; ++j) {
+          const int dim = DOD * 16 * (lane >> 4) + 16 * j + (lane & 15);
+          if (out) a.out[(int64_t)e.dst * a.out_stride + (int64_t)(head0 + h) * D + dim] = (uint16_t)bf16_bits(e.v[h][j]);
+          else a.part_o[(part + h) * D + dim] = e.v[h][j];
+        }
+      }
+    } else {
 #pragma unroll
-        for (int c = 0; c < S::NO; ++c) dst[16 * c] = e.v[c][r];
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * q + r;
+        if (h >= hv) continue;
+        if (out) {
+          uint16_t* dst = a.out + (int64_t)e.dst * a.out_stride + (int64_t)(head0 + h) * D + c16;
+#pragma unroll
+          for (int c = 0; c < S::NO; ++c) dst[16 * c] = (uint16_t)bf16_bits(e.v[c][r]);
+        } else {
+          float* dst = a.part_o + (part + h) * D + c16;
+#pragma unroll
+          for (int c = 0; c < S::NO; ++c) dst[16 * c] = e.v[c][r];
+        }
       }
     }
     if (!out && q == 0 && c16 < hv) {
@@ -476,11 +539,17 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   };
 
   auto finalize = [&](const TileDesc& t) {
-    l_run = col4_sum(l_run);
     float lrow[4];
+    float lt[kDotMaxHeads];
+    if constexpr (DOT) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      lrow[r] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l_run)));
+      for (int h = 0; h < kDotMaxHeads; ++h) lt[h] = key32_sum(dl[h]);
+    } else {
+      l_run = col4_sum(l_run);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        lrow[r] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * q + r) << 2, __float_as_int(l_run)));
+    }
     const int kvh = kv_head_of(t), hg = t.h - kvh * a.head_groups;
     const int hv = min(16, a.group - hg * 16);
     const int head0 = kvh * a.group + hg * 16;
@@ -491,23 +560,40 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
       npend = 1;
     }
     Pending e;
-    e.m = m_run;
-    e.l = l_run;
-    if (g0 >= g_begin && g0 + row_tiles<TS>(t.ctx, a.window).count <= g_end) {
+    const bool whole = g0 >= g_begin && g0 + row_tiles<TS>(t.ctx, a.window).count <= g_end;
+    if constexpr (DOT) {
+      // Lane h (< hv) carries head h's max and sum.
+      e.m = lane == 0 ? dm_run[0] : lane == 1 ? dm_run[1] : dm_run[2];
+      e.l = lane == 0 ? lt[0] : lane == 1 ? lt[1] : lt[2];
+#pragma unroll
+      for (int h = 0; h < kDotMaxHeads; ++h) {
+        const float inv = whole ? (lt[h] > 0.f ? 1.f / lt[h] : 0.f) : 1.f;
+#pragma unroll
+        for (int j = 0; j < DOD; ++j) e.v[h][j] = od[h][j] * inv;
+      }
+    } else {
+      e.m = m_run;
+      e.l = l_run;
+    }
+    if (whole) {
       e.kind = hv | 32 | (head0 << 6);
       e.dst = t.qrow;
-      float inv[4];
+      if constexpr (!DOT) {
+        float inv[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) inv[r] = lrow[r] > 0.f ? 1.f / lrow[r] : 0.f;
+        for (int r = 0; r < 4; ++r) inv[r] = lrow[r] > 0.f ? 1.f / lrow[r] : 0.f;
 #pragma unroll
-      for (int c = 0; c < S::NO; ++c)
+        for (int c = 0; c < S::NO; ++c)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) e.v[c][r] = o[c][r] * inv[r];
+          for (int r = 0; r < 4; ++r) e.v[c][r] = o[c][r] * inv[r];
+      }
     } else {
       e.kind = hv;
       e.dst = 2 * w + (g0 <= g_begin ? 0 : 1);  // partial slot
+      if constexpr (!DOT) {
 #pragma unroll
-      for (int c = 0; c < S::NO; ++c) e.v[c] = o[c];
+        for (int c = 0; c < S::NO; ++c) e.v[c] = o[c];
+      }
     }
     e.span = -1;
     e.span0 = e.span1 = 0;
@@ -531,21 +617,150 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   auto read_query = [&](const TileDesc& t, const char* qsb) {
     const int hg = t.h - kv_head_of(t) * a.head_groups;
     const int hv = min(16, a.group - hg * 16);
+    if constexpr (DOT) {
+      // Head h's half (lane / 32) of the dims, as DNC 16-byte chunks.
+      const int half = lane >> 5;
 #pragma unroll
-    for (int c = 0; c < S::NC; ++c) {
-      bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(qsb + c16 * (2 * D) + (4 * c + q) * 16);
-      qb[c] = c16 < hv ? v : bf16x8_t{};
+      for (int h = 0; h < kDotMaxHeads; ++h)
+#pragma unroll
+        for (int i = 0; i < DNC; ++i)
+          qd[h][i] = h < hv ? *reinterpret_cast<const u32x4_t*>(qsb + h * (2 * D) + (half * DNC + i) * 16)
+                            : u32x4_t{0u, 0u, 0u, 0u};
+    } else {
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c) {
+        bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(qsb + c16 * (2 * D) + (4 * c + q) * 16);
+        qb[c] = c16 < hv ? v : bf16x8_t{};
+      }
+    }
+  };
+  // Masked keys of a tile hold arbitrary pool data: zero their V rows so that
+  // a zero probability cannot meet a non-finite value.
+  auto zero_masked_v = [&](const TileDesc& t, char* vt) {
+    if (t.tb < t.left || t.tb + TS > t.ctx) {
+#pragma unroll
+      for (int i = 0; i < S::LOADS; ++i) {
+        const int s = i * 64 + lane;
+        const int key = t.tb + s / S::CPR;
+        if (key < t.left || key >= t.ctx) *reinterpret_cast<uint4*>(vt + s * 16) = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  // Dot form of one tile: Q.K per key, online softmax per head, P.V per dim.
+  auto dot_tile = [&](const TileDesc& t, const char* kt, char* vt) {
+    const int kvh = kv_head_of(t), hg = t.h - kvh * a.head_groups;
+    const int hv = min(16, a.group - hg * 16);
+    const int key = lane & 31, half = lane >> 5;
+    u32x4_t kc[DNC];
+#pragma unroll
+    for (int i = 0; i < DNC; ++i)
+      kc[i] = *reinterpret_cast<const u32x4_t*>(kt + key * (2 * D) + (((half * DNC + i) ^ swz(key, D / 8)) << 4));
+    float sd[kDotMaxHeads];
+#pragma unroll
+    for (int h = 0; h < kDotMaxHeads; ++h) {
+      sd[h] = -INFINITY;
+      if (h >= hv) continue;  // uniform
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < DNC; ++i) {
+        a0 = dot2(qd[h][i][0], kc[i][0], a0);
+        a1 = dot2(qd[h][i][1], kc[i][1], a1);
+        a0 = dot2(qd[h][i][2], kc[i][2], a0);
+        a1 = dot2(qd[h][i][3], kc[i][3], a1);
+      }
+      const float part = a0 + a1;
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(part), __float_as_uint(part), false, false);
+      float sv = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      if constexpr (SOFTCAP) sv = a.softcap_log2 * soft_tanh(sv * a.score_scale);
+      const int k = t.tb + key;
+      sd[h] = (SOFTCAP || !(t.tb >= t.left && t.tb + TS <= t.ctx)) ? ((k >= t.left && k < t.ctx) ? sv : -INFINITY)
+                                                                    : sv;
+    }
+    // Re-base each head whose tile maximum passes its threshold.
+    float mx[kDotMaxHeads];
+    bool any = false;
+#pragma unroll
+    for (int h = 0; h < kDotMaxHeads; ++h) {
+      mx[h] = h < hv ? key32_max(sd[h]) : -INFINITY;
+      any = any || mx[h] > (SOFTCAP ? dm_run[h] + kDecodeRescaleSlack : dm_thr[h]);
+    }
+    if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+      for (int h = 0; h < kDotMaxHeads; ++h) {
+        if (!(mx[h] > (SOFTCAP ? dm_run[h] + kDecodeRescaleSlack : dm_thr[h]))) continue;  // uniform
+        const float m_new = fmaxf(dm_run[h], SOFTCAP ? mx[h] : mx[h] * a.score_scale);
+        const float alpha = dm_run[h] == -INFINITY ? 0.f : fast_exp2(dm_run[h] - m_new);
+        dl[h] *= alpha;
+#pragma unroll
+        for (int j = 0; j < DOD; ++j) od[h][j] *= alpha;
+        dm_run[h] = m_new;
+        dm_thr[h] = (m_new + kDecodeRescaleSlack) * inv_scale;
+        dm_base[h] = m_new == -INFINITY ? 0.f : m_new;
+      }
+    }
+    // Probabilities (fp32 into the sums, bf16 into P.V), packed by key pairs:
+    // lane 2k of each half holds keys (2k, 2k + 1) of every head.
+    uint32_t pp[kDotMaxHeads];
+#pragma unroll
+    for (int h = 0; h < kDotMaxHeads; ++h) {
+      const float p = SOFTCAP ? fast_exp2(sd[h] - dm_base[h]) : fast_exp2(__builtin_fmaf(sd[h], a.score_scale, -dm_base[h]));
+      dl[h] += h < hv ? p : 0.f;
+      const uint32_t b = bf16_bits(p);
+      const uint32_t nb = __float_as_uint(dpp<kDppQuadXor1>(__uint_as_float(b)));
+      pp[h] = b | (nb << 16);
+    }
+    zero_masked_v(t, vt);
+    // P.V: the 16-lane group g = lane / 16 reads, for key quad kq, the 4 x 16
+    // block of keys 4 kq .. + 3 and dims 32 g + 16 j .. + 15 (D = 128;
+    // 16 g .. + 15 at D = 64) transposed: lane i of the group receives dim
+    // d_j = block start + i for the four keys.
+    const int grp = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int kq = 0; kq < TS / 4; ++kq) {
+      const int tk = 4 * kq + (i16 >> 2);
+#pragma unroll
+      for (int j = 0; j < DOD; ++j) {
+        const int c0 = DOD * 16 * grp + 16 * j;  // first dim of the block
+        const int lc = c0 / 8 + ((i16 & 3) >> 1);
+        const bf16x4_t v = lds_read_tr4(vt + tk * (2 * D) + ((lc ^ swz(tk, D / 8)) << 4) + ((i16 & 1) << 3));
+        const auto vw = __builtin_bit_cast(u32x2_t, v);
+#pragma unroll
+        for (int h = 0; h < kDotMaxHeads; ++h) {
+          if (h >= hv) continue;  // uniform
+          const uint32_t p01 = __builtin_amdgcn_readlane(pp[h], 4 * kq);
+          const uint32_t p23 = __builtin_amdgcn_readlane(pp[h], 4 * kq + 2);
+          od[h][j] = dot2(vw[1], p23, dot2(vw[0], p01, od[h][j]));
+        }
+      }
     }
   };
   auto consume = [&](const TileDesc& t, const char* kt, char* vt, int qpar_t) {
     if (t.flags & kTileFirst) {
       read_query(t, qs[qpar_t]);
+      if constexpr (DOT) {
 #pragma unroll
-      for (int c = 0; c < S::NO; ++c) o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      m_run = -INFINITY;
-      l_run = 0.f;
-      m_thr = -INFINITY;
-      m_base = 0.f;
+        for (int h = 0; h < kDotMaxHeads; ++h) {
+#pragma unroll
+          for (int j = 0; j < DOD; ++j) od[h][j] = 0.f;
+          dm_run[h] = -INFINITY;
+          dm_thr[h] = -INFINITY;
+          dm_base[h] = 0.f;
+          dl[h] = 0.f;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < S::NO; ++c) o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        m_run = -INFINITY;
+        l_run = 0.f;
+        m_thr = -INFINITY;
+        m_base = 0.f;
+      }
+    }
+    if constexpr (DOT) {
+      dot_tile(t, kt, vt);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (t.flags & kTileLast) finalize(t);
+      return;
     }
 
     // K tile -> registers as the A operand of S^T: lane (q, c16), group h holds
@@ -612,16 +827,7 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
         l_run += p;
       }
 
-    // Masked keys of a tile hold arbitrary pool data: zero their V rows so that
-    // a zero probability cannot meet a non-finite value.
-    if (t.tb < t.left || t.tb + TS > t.ctx) {
-#pragma unroll
-      for (int i = 0; i < S::LOADS; ++i) {
-        const int s = i * 64 + lane;
-        const int key = t.tb + s / S::CPR;
-        if (key < t.left || key >= t.ctx) *reinterpret_cast<uint4*>(vt + s * 16) = make_uint4(0, 0, 0, 0);
-      }
-    }
+    zero_masked_v(t, vt);
 
     if constexpr (TS == 32) {
       bf16x8_t pa;
@@ -722,6 +928,15 @@ __global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
   if (kMaxPend > 0 && npend == 2) flush(pend1);
 }
 
+template <int D, bool SOFTCAP, int MODE>
+__global__ __launch_bounds__(64, 1) void decode_stream_kernel(StreamArgs sa) {
+  decode_stream_body<D, SOFTCAP, MODE, kArithMfma>(sa);
+}
+template <int D, bool SOFTCAP, int MODE>
+__global__ __launch_bounds__(64, 1) void decode_stream_dot_kernel(StreamArgs sa) {
+  decode_stream_body<D, SOFTCAP, MODE, kArithDot>(sa);
+}
+
 // ---------------------------------------------------------------------------
 // Merge of the units that span workgroups
 // ---------------------------------------------------------------------------
@@ -818,6 +1033,15 @@ int resident_per_cu(bool softcap, int mode) {
 
 template <int D, int MODE>
 void launch_stream_mode(const StreamArgs& sa, bool softcap, dim3 grid, hipStream_t stream) {
+#if GK_STREAM_DOT
+  if constexpr (D <= 128) {
+    if (sa.d.heads_per_group <= kDotMaxHeads) {
+      if (softcap) decode_stream_dot_kernel<D, true, MODE><<<grid, 64, 0, stream>>>(sa);
+      else decode_stream_dot_kernel<D, false, MODE><<<grid, 64, 0, stream>>>(sa);
+      return;
+    }
+  }
+#endif
   if (softcap) decode_stream_kernel<D, true, MODE><<<grid, 64, 0, stream>>>(sa);
   else decode_stream_kernel<D, false, MODE><<<grid, 64, 0, stream>>>(sa);
 }

@@ -60,6 +60,8 @@ CONFIGS = {
     "c2g2": (64, 16, 8, 128, 128, 4096, lambda rng, b: rng.integers(512, 4097, b)),
     # ... and at group 1 (8 q / 8 kv heads, multi-head attention).
     "c2g1": (64, 8, 8, 128, 128, 4096, lambda rng, b: rng.integers(512, 4097, b)),
+    # ... and at group 3 (24 q / 8 kv heads), the largest group below a dense MFMA tile.
+    "c2g3": (64, 24, 8, 128, 128, 4096, lambda rng, b: rng.integers(512, 4097, b)),
 }
 
 

@@ -183,6 +183,23 @@ def test_stream_window_and_softcap(runner, variant, block):
     check(case, runner.run_case(case), fp32_softmax=True)
 
 
+@pytest.mark.parametrize("geometry", [(8, 8, 128), (6, 3, 64), (9, 3, 128), (4, 2, 64)])
+@pytest.mark.parametrize("block", [1, 4, 32])
+@pytest.mark.parametrize("variant", ["plain", "window", "softcap", "both"])
+def test_stream_small_groups_window_softcap_blocks(runner, geometry, variant, block):
+    # GQA groups 1-3: units of one to three query heads, with a window that
+    # starts inside a tile, softcap, short rows and sub-tile blocks.
+    heads, kv_heads, d = geometry
+    lens = np.array([1, 31, 33, 40, 300, 1000, 64, 65, 2100])
+    case = cases.decode_case(heads * 100 + d + block, len(lens), heads, kv_heads, d, block, 16384 // block, lens)
+    if variant in ("window", "both"):
+        case.window = 77
+    if variant in ("softcap", "both"):
+        case.softcap = 30.0
+    print("geometry", geometry, "block", block, variant, flush=True)
+    check(case, runner.run_case(case), fp32_softmax=variant != "plain")
+
+
 def test_stream_window_head_dim_256(runner):
     lens = np.array([40, 300, 1000, 64, 65])
     case = cases.decode_case(99, len(lens), 8, 2, 256, 32, 256, lens)
