@@ -55,8 +55,8 @@ CONFIGS = {
     "c3": (256, 32, 8, 128, 128, None, lambda rng, b: rng.integers(128, 2049, b)),
     "c5": (32, 64, 8, 128, 128, 8192,
            lambda rng, b: np.rint(np.exp(rng.uniform(math.log(1024), math.log(32768), b))).astype(np.int64)),
-    # C2's batch, lengths, pool and KV bytes at GQA group 2 (16 q / 8 kv heads):
-    # the geometry the wave-level dot-product kernel serves.
+    # C2's batch, lengths, pool and KV bytes at GQA group 2 (16 q / 8 kv heads),
+    # where most of the decode MFMA tile's 16 head columns are padding.
     "c2g2": (64, 16, 8, 128, 128, 4096, lambda rng, b: rng.integers(512, 4097, b)),
     # ... and at group 1 (8 q / 8 kv heads, multi-head attention).
     "c2g1": (64, 8, 8, 128, 128, 4096, lambda rng, b: rng.integers(512, 4097, b)),

@@ -87,10 +87,11 @@ typedef struct gk_decode_params {
   float softcap;               /* 0 = off */
   int32_t sliding_window;      /* <= 0 = off */
   int32_t max_context;         /* host bound: row_context[r] <= max_context for every row */
-  int32_t partition_tokens;    /* split-K partition (multiple of 32); 0 = library choice: for
-                                  GQA groups >= 4 (any block_size) a balanced split of all
-                                  key tiles over one resident grid, otherwise a partition
-                                  sized from the batch; either way a row's split points,
+  int32_t partition_tokens;    /* split-K partition (multiple of 32); 0 = library choice: a
+                                  balanced split of all key tiles over one resident grid
+                                  (any GQA group and block_size), or a partition sized from
+                                  the batch for batches beyond the split's 32-bit tile
+                                  numbering; either way a row's split points,
                                   and so its last bits, depend on the whole batch. A fixed
                                   partition (> 0) makes every row's output a function of
                                   that row alone, bit for bit (batch-invariant decode) */

@@ -1,7 +1,7 @@
 """GPU parity of the balanced decode schedule (gk_paged_decode with partition_tokens = 0).
 
-With the partition left to the library and GQA groups >= 4 (any block size,
-the token-granular map included), gk_paged_decode splits the batch's
+With the partition left to the library (any GQA group and block size, the
+token-granular map included), gk_paged_decode splits the batch's
 key tiles evenly over one resident grid: work units (row, kv head) are cut at
 arbitrary tiles, partial states are merged with the log-sum-exp rule, and the
 tiles of a unit are visited in rotated order. These cases pin every piece of
