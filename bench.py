@@ -35,7 +35,6 @@ to the GPU time of the same step. It prints its own JSON line.
 import argparse
 import ctypes
 import json
-import math
 import os
 import statistics
 import sys

@@ -13,7 +13,6 @@ import numpy as np
 
 from oracle import oracle as orc
 from gaudirt_amd.workloads import permuted_block_tables  # noqa: F401  (re-exported)
-from gaudirt_amd import workloads
 
 
 def bf16_normal(rng, shape):

@@ -9,7 +9,6 @@ synthetic geometries allow one bf16 ulp where it exceeds 2e-2 (|out| >= 4),
 where even the exact answer rounded to bf16 can differ from direct_bf16_pv.
 """
 
-import math
 
 import numpy as np
 import pytest

@@ -1,7 +1,5 @@
 """GPU parity of the KV store, tile-index and decode-length kernels (C ABI): bit-exact."""
 
-import ctypes
-
 import numpy as np
 import pytest
 
