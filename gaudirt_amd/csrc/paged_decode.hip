@@ -48,13 +48,18 @@ namespace gk {
 namespace {
 
 constexpr int kWaves = 4;
-// Waves per SIMD the MFMA kernel is compiled for: 3 bounds its registers to
-// 168 (head_dim <= 128); head_dim 256 holds twice the accumulators and gets 2.
+// Waves per SIMD the MFMA kernel is compiled for: 3 at head_dim 64 (92
+// registers). At head_dim 128 and 256 its LDS (two K and two V stages, 32 KiB
+// at head_dim 128) keeps at most five workgroups on a CU, so a target of 3
+// would only bound the registers: head_dim 128 needs 216 (184 VGPRs and 32
+// AGPRs), missed that target and ran at 2 anyway, and compiled for 2 it
+// measured C5 at 2048-key partitions 240.2-240.6 -> 236.3-236.4 us (C2
+// 111.6-111.7 -> 111.2-111.6).
 #ifndef GK_MFMA_WAVES_PER_SIMD
 #define GK_MFMA_WAVES_PER_SIMD 3
 #endif
 template <int D>
-constexpr int mfma_waves_per_simd() { return D == 256 ? 2 : GK_MFMA_WAVES_PER_SIMD; }
+constexpr int mfma_waves_per_simd() { return D >= 128 ? 2 : GK_MFMA_WAVES_PER_SIMD; }
 
 
 __device__ __forceinline__ uint32_t word(const uint4& v, int e) {
