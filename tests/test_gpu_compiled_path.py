@@ -176,3 +176,53 @@ def test_validated_entry_under_torch_compile(torch_ext):
         assert np.array_equal(bits(torch, pool), want_pool), seed
         print("compiled call", seed, "equals eager", flush=True)
     del gaudirt_amd
+
+
+def test_dispatch_smoke_tensors_outlive_their_metadata(torch_ext):
+    """tests/paged_attention_dispatch_smoke.py: single decode rows at positions
+    18, 254, 255, 511 and 18 again (56 q / 8 kv heads, head_dim 128, one request
+    whose token t sits at slot t + 1 of a 1026-slot pool), each through
+    _paged_attn_validated after the PagedMetadata object that produced the
+    tensors has been deleted and collected: the slots, requests, positions,
+    plan and header keep their storage, and every step matches the oracle on
+    the pool as stored. The smoke hands the request map where the plan goes;
+    the reference's plan check (src/bridge/attention_plan.cpp:132-140) rejects
+    such a tensor, and so does this op, with the same message and before any KV
+    write."""
+    import gc
+
+    import gaudirt_amd
+
+    torch = torch_ext
+    heads, kv_heads, dim, context = 56, 8, 128, 1024
+    slots = context + 2
+    gen = torch.Generator().manual_seed(1907)
+    mapping = torch.arange(1, context + 1, dtype=torch.int32).view(1, context)
+    pool = gaudirt_amd.allocate_paged_kv(1, slots, kv_heads, dim)
+    key_pool, value_pool = gaudirt_amd.kv_pool_views(pool, 0)
+    query = torch.randn((1, heads * dim), generator=gen).to(torch.bfloat16).cuda()
+    key = torch.randn((1, kv_heads * dim), generator=gen).to(torch.bfloat16).cuda()
+    value = torch.randn((1, kv_heads * dim), generator=gen).to(torch.bfloat16).cuda()
+    scale = float(np.float32(1 / math.sqrt(dim)))
+    op = torch.ops.gaudirt._paged_attn_validated.default
+    for position in (18, 254, 255, 511, 18):
+        meta = torch.classes.gaudirt.PagedMetadata(torch.tensor([position + 1]), torch.tensor([0]),
+                                                   torch.tensor([position]), mapping, slots)
+        locations, requests, positions = meta.row_locations(), meta.row_requests(), meta.rotary_positions()
+        plan, header = meta.attention_plan(heads, kv_heads, dim), meta.rotary_header()
+        request_map = meta.request_mapping()
+        del meta
+        gc.collect()
+        before = bits(torch, pool)
+        with pytest.raises(RuntimeError, match="invalid or expired metadata plan"):
+            op(query, key, value, key_pool, value_pool, locations, requests, positions, request_map, header, dim,
+               scale)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(torch, pool), before)
+        out = op(query, key, value, key_pool, value_pool, locations, requests, positions, plan, header, dim, scale)
+        torch.cuda.synchronize()
+        stored = bits(torch, pool)[0]
+        problem = orc.Problem(bits(torch, query), stored, np.array([0]), np.array([position]), mapping.numpy(), heads,
+                              kv_heads, dim, scale)
+        max_abs, mean_abs = orc.check_flat_gate(bits(torch, out), orc.direct_bf16_pv(problem))
+        print("position", position, f"max_abs={max_abs:.3e} mean_abs={mean_abs:.3e}", flush=True)

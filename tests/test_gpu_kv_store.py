@@ -87,6 +87,8 @@ def test_tile_indices_reference_device_cases(runner, requests_n, context, slots)
 
 @pytest.mark.parametrize("count", [1, 3, 16, 70000])
 def test_advance_decode_lengths(runner, count):
+    # tests/decode_lengths_smoke.py's counts and values (int64 lengths past
+    # 2^32), plus a count past one workgroup; the inputs stay as they were.
     import torch
     from gaudirt_amd import capi
     seq = torch.arange(count, dtype=torch.int64) * (2**33) + 17

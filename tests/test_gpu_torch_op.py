@@ -257,6 +257,31 @@ def test_advance_decode_lengths_op(torch_ext):
         torch.ops.gaudirt._advance_decode_lengths(orig, seq)
 
 
+def test_advance_decode_lengths_op_captured(torch_ext):
+    # tests/decode_lengths_smoke.py counts one launch and no host copies per
+    # call, with the old batch's tensors kept. Captured in a HIP graph (a host
+    # copy or a synchronisation inside would fail the capture) and replayed with
+    # new inputs copied in between.
+    torch = torch_ext
+    for count in (1, 3, 16):
+        seq = (torch.arange(count, dtype=torch.int64) * (2**33) + 17).cuda()
+        orig = (torch.arange(count, dtype=torch.int32) + 31).cuda()
+        torch.ops.gaudirt._advance_decode_lengths(seq, orig)  # warm-up outside capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            nxt, onxt = torch.ops.gaudirt._advance_decode_lengths(seq, orig)
+        for step in range(3):
+            host_seq = torch.arange(count, dtype=torch.int64) * (2**33) + 17 + step * 1000
+            host_orig = torch.arange(count, dtype=torch.int32) + 31 + step
+            seq.copy_(host_seq)
+            orig.copy_(host_orig)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(nxt.cpu(), host_seq + 1) and torch.equal(onxt.cpu(), host_orig + 1)
+            assert torch.equal(seq.cpu(), host_seq) and torch.equal(orig.cpu(), host_orig)
+
+
 def test_kv_pool_allocation_and_reuse(torch_ext):
     # tests/paged_kv_pool_smoke.py: geometry, zero init, layer-view addresses.
     import gaudirt_amd
