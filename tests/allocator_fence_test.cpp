@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <map>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -225,6 +226,43 @@ int main() {
     CHECK(rt.created == warm);
     CHECK(rt.waits.size() > waits_before);  // the cycles did fence
     CHECK(pool.stats().allocated_bytes == 0);
+  }
+  {  // tests/block_allocator_device_test.cpp:27-58: 256-byte blocks and their
+     // accounting, a neighbour merge, the whole slab coalescing back after a
+     // random allocate/free stress, and peak accounting (one stream: no fence).
+    MockRuntime rt;
+    constexpr uint64_t slab = 4 << 20;
+    gk::BlockAllocator pool(rt, slab, slab);
+    void* a = alloc(pool, 1, 1);
+    void* b = alloc(pool, 257, 1);
+    void* c = alloc(pool, 9, 1);
+    CHECK(pool.stats().allocated_bytes == 1024);
+    release(pool, b);
+    release(pool, a);
+    void* merged = alloc(pool, 768, 1);
+    CHECK(merged == a);
+    release(pool, merged);
+    release(pool, c);
+    void* entire = alloc(pool, slab, 1);
+    CHECK(entire == a);
+    release(pool, entire);
+    std::mt19937 rng(12345);
+    std::vector<void*> live;
+    for (int i = 0; i < 2000; ++i) {
+      if (!live.empty() && rng() % 2) {
+        const size_t index = rng() % live.size();
+        release(pool, live[index]);
+        live.erase(live.begin() + static_cast<std::ptrdiff_t>(index));
+      } else {
+        live.push_back(alloc(pool, 1 + rng() % 2048, 1));
+      }
+    }
+    for (void* p : live) release(pool, p);
+    entire = alloc(pool, slab, 1);
+    CHECK(entire == a);
+    release(pool, entire);
+    CHECK(pool.stats().allocated_bytes == 0 && pool.stats().peak_bytes == slab && pool.stats().slabs == 1);
+    CHECK(rt.created == 0 && rt.waits.empty());
   }
   std::printf("OK\n");
   return 0;
