@@ -61,7 +61,11 @@ WORKLOADS = {
             "4096-block bf16 pool",
     "c2g3": "c2 at GQA group 3: batch 64, 24 q / 8 kv heads, head_dim 128, block 128, ctx U[512,4096], "
             "4096-block bf16 pool",
+    "c4d256": "c4 at head_dim 256 (Gemma-2-9B-shaped heads): 8 sequences x 512-row causal chunks on a shared "
+              "2048-token prefix, 16 q / 8 kv heads, head_dim 256, block 128",
 }
+# Prefill workloads: DevicePrefillCase arguments besides the C4 defaults.
+PREFILL_WORKLOADS = {"c4": {}, "c4d256": {"heads": 16, "kv_heads": 8, "head_dim": 256}}
 C4_WARMUP = 1000
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
@@ -97,6 +101,7 @@ DOMINANT_KERNEL = {
     "c3": "decode_stream_kernel<128, false, 0>",
     "c5": "decode_stream_kernel<128, false, 0>",
     "c4": "prefill_kernel<128, false, 0>",
+    "c4d256": "prefill_kernel<256, false, 0>",
 }
 
 
@@ -185,14 +190,14 @@ def host_cpu():
             + (f", OMP_NUM_THREADS={omp}" if omp else "") + ")")
 
 
-def prefill_run(lib, steps, warmup, seed):
-    """Workload C4: one gk_paged_prefill call per step, timed with HIP events on the
-    launch stream. Returns (ms per step, TFLOP/s, the case)."""
+def prefill_run(lib, steps, warmup, seed, workload="c4"):
+    """A prefill workload (C4): one gk_paged_prefill call per step, timed with HIP
+    events on the launch stream. Returns (ms per step, TFLOP/s, the case)."""
     import torch
 
     from gaudirt_amd import capi, workloads
 
-    pc = workloads.DevicePrefillCase(seed=seed)
+    pc = workloads.DevicePrefillCase(seed=seed, **PREFILL_WORKLOADS[workload])
     stream = torch.cuda.current_stream()
     p = capi.PrefillParams()
     p.query, p.q_row_stride = pc.query.data_ptr(), pc.query.stride(0)
@@ -216,27 +221,28 @@ def prefill_run(lib, steps, warmup, seed):
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
     tflops = pc.flops() / (ms * 1e-3) / 1e12
-    print(f"[bench] c4: {ms * 1e3:.1f} us/step, {tflops:.1f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of "
+    print(f"[bench] {workload}: {ms * 1e3:.1f} us/step, {tflops:.1f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of "
           f"{MFMA_BF16_PEAK_TFLOPS:.0f}), {pc.rows / (ms * 1e-3):.4g} query rows/s", file=sys.stderr, flush=True)
     return ms, tflops, pc
 
 
-def prefill_roofline(tflops):
+def prefill_roofline(tflops, workload="c4"):
     return {"bound": "mfma", "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": measured_traffic("c4")}
+            "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": measured_traffic(workload)}
 
 
 def prefill_bench(args):
-    """C4 as the headline workload: its own JSON line (MFMA roofline, causal-exact FLOPs)."""
+    """A prefill workload as the headline: its own JSON line (MFMA roofline, causal-exact FLOPs)."""
     from gaudirt_amd import capi
 
-    ms, tflops, pc = prefill_run(capi.load(), args.steps, args.warmup, args.seed)
+    w = args.workload
+    ms, tflops, pc = prefill_run(capi.load(), args.steps, args.warmup, args.seed, w)
     print(json.dumps({
         "metric": "prefix-shared chunked prefill attention TFLOP/s (causal-exact), 1 MI355X",
         "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic", "config": {"workload": f"c4: {WORKLOADS['c4']}", "flops_per_step": pc.flops()},
-        "roofline": prefill_roofline(tflops), "cpu_baseline": None}), flush=True)
+        "data": "synthetic", "config": {"workload": f"{w}: {WORKLOADS[w]}", "flops_per_step": pc.flops()},
+        "roofline": prefill_roofline(tflops, w), "cpu_baseline": None}), flush=True)
 
 
 def decode_run(lib, workload, steps, warmup, table_sets, seed, partition, page_size=0):
@@ -457,7 +463,7 @@ def main():
               "the decode path does not shard across GPUs here", file=sys.stderr)
         sys.exit(2)
     if args.warmup is None:
-        args.warmup = C4_WARMUP if args.workload == "c4" else 20
+        args.warmup = C4_WARMUP if args.workload in PREFILL_WORKLOADS else 20
 
     import torch
 
@@ -465,7 +471,7 @@ def main():
     torch.cuda.set_device(0)
     if args.host_overhead:
         return host_overhead(args)
-    if args.workload == "c4":
+    if args.workload in PREFILL_WORKLOADS:
         return prefill_bench(args)
 
     from gaudirt_amd import capi

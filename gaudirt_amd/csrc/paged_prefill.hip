@@ -8,9 +8,10 @@
 //
 // Work decomposition. A workgroup of eight waves owns one (sequence, kv head,
 // tile of rows). The GQA group is folded into the tile: its 256 "query rows"
-// are (row, head) pairs, so one K/V tile serves every head of the group. Each
-// wave computes 32 query rows (two 16-column MFMA tiles) against the keys of
-// a step (64 at head_dim 128, 32 at head_dim 64):
+// (128 at head_dim 256) are (row, head) pairs, so one K/V tile serves every
+// head of the group. Each wave computes 32 query rows (two 16-column MFMA
+// tiles; one, 16 rows, at head_dim 256) against the keys of a step (64 at
+// head_dim 128, 32 at head_dim 64 and 256):
 //   S^T[key][qrow] = K . Q^T      v_mfma_f32_16x16x32_bf16, K from LDS
 //   O[qrow][dim]  += P . V        P straight from S^T's registers, V read
 //                                 transposed from LDS (ds_read_b64_tr_b16)
@@ -39,18 +40,25 @@ namespace {
 // same box: 180.0 -> 174.1 us with four -> eight waves; 168.8 us together with
 // the early V reads below).
 constexpr int kPrefillWaves = 8;
-// 16-column query tiles per wave. Two: three fit in 256 VGPRs only without the
-// early V reads, and four spill; both also quantise C4's rows badly (48- or
-// 64-row tiles of 512-row chunks leave a partial round of workgroups).
+// 16-column query tiles per wave. Two at head_dim 64 and 128: three fit in 256
+// VGPRs only without the early V reads, and four spill; both also quantise
+// C4's rows badly (48- or 64-row tiles of 512-row chunks leave a partial round
+// of workgroups). One at head_dim 256, whose output accumulators alone take 64
+// VGPRs per tile: with two, every head_dim 256 instance spills 536-588 bytes
+// per lane.
 constexpr int kNT = 2;
 constexpr int kQrowsPerWave = 16 * kNT;
-constexpr int kQrows = kPrefillWaves * kQrowsPerWave;     // query rows per workgroup
+template <int D>
+constexpr int prefill_nt() { return D > 128 ? 1 : kNT; }
+// Query rows per workgroup at head dimension d.
+constexpr int prefill_qrows(int d) { return kPrefillWaves * 16 * (d > 128 ? 1 : kNT); }
 // Keys per step: 64 at head_dim 128 (half the per-step barriers, cross-lane
 // maxima, re-base checks and load setup of 32-key steps: C4 178.1 -> 166.8
 // us); 32 at head_dim 64, whose 64-key form needs 130 VGPRs and so would drop
-// from four waves per SIMD to three.
+// from four waves per SIMD to three, and at head_dim 256, where a 64-key K
+// and V tile pair takes 64 KiB of LDS per stage.
 template <int D>
-constexpr int prefill_keys() { return D >= 128 ? 64 : 32; }
+constexpr int prefill_keys() { return D == 128 ? 64 : 32; }
 // K/V pipeline depth. Two: three and four stages measured the same on C4 (the
 // kernel is bound by its instruction stream, not by load latency).
 constexpr int kStages = 2;
@@ -122,6 +130,8 @@ constexpr int kStepBlocks = 0, kLoadBlocks = 1, kKeyBlocks = 2;
 template <int D, bool SOFTCAP, int MODE>
 __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
   using S = PrefillShape<D>;
+  // This head dimension's query tiles per wave (in place of the namespace's).
+  constexpr int kNT = prefill_nt<D>(), kQrowsPerWave = 16 * kNT;
   constexpr int kKeys = prefill_keys<D>();
   static_assert(kKeys == 32 || kKeys == 64, "a step is one or two 32-key halves");
   constexpr int kKG = kKeys / 16;  // 16-key groups per step (Q.K tiles)
@@ -141,8 +151,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   // pieces for the global stores. Being separate from the stages, a wave
   // starts its output as soon as its own last step ends, with no barrier
   // (132 KiB at head_dim 128, one workgroup per CU either way).
-  constexpr bool kLag = GK_PREFILL_LAG && D >= 128 && !SOFTCAP;  // softcap: no registers to spare
-  constexpr bool kPipe = GK_PREFILL_PIPE && D >= 128 && !SOFTCAP && !kLag;
+  constexpr bool kLag = GK_PREFILL_LAG && D == 128 && !SOFTCAP;  // softcap: no registers to spare
+  constexpr bool kPipe = GK_PREFILL_PIPE && D == 128 && !SOFTCAP && !kLag;
   constexpr int kOutRowBytes = 2 * D + 16;
   constexpr int kKvBytes = (kLag ? 5 : kStages * 2) * S::TILE,
                 kOutBytes = kPrefillWaves * kQrowsPerWave * kOutRowBytes;
@@ -783,11 +793,17 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
         if (step + 2 < nsteps) e_next = entry_of(tb + 2 * kKeys);
       }
       scores(kv[cur][0]);
-      bf16x8_t vfirst[S::NO];
+      if constexpr (D <= 128) {
+        bf16x8_t vfirst[S::NO];
 #pragma unroll
-      for (int c = 0; c < S::NO; ++c) vfirst[c] = read_v(kv[cur][1], 0, c);
-      softmax(tb);
-      accumulate(kv[cur][1], vfirst);
+        for (int c = 0; c < S::NO; ++c) vfirst[c] = read_v(kv[cur][1], 0, c);
+        softmax(tb);
+        accumulate(kv[cur][1], vfirst);
+      } else {
+        // head_dim 256: the early V reads would take 64 more VGPRs.
+        softmax(tb);
+        accumulate(kv[cur][1], nullptr);
+      }
     };
     int step = 0;
     for (; step + 1 < nsteps; step += 2) {
@@ -1324,8 +1340,8 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
   if (!p) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: null parameters");
   if (p->struct_size != sizeof(gk_prefill_params))
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: struct_size does not match this library's gk_prefill_params");
-  if (p->head_dim != 64 && p->head_dim != 128)
-    return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: head dimension must be 64 or 128");
+  if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256)
+    return fail(GK_ERR_UNSUPPORTED, "gk_paged_prefill: head dimension must be 64, 128 or 256");
   if (p->q_heads <= 0 || p->kv_heads <= 0 || p->q_heads % p->kv_heads || p->q_heads / p->kv_heads > 128)
     return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: invalid head geometry (GQA group at most 128)");
   if (!is_pow2(p->block_size) || p->block_size > (1 << 20))
@@ -1360,7 +1376,7 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
   a.q_heads = p->q_heads;
   a.kv_heads = p->kv_heads;
   a.group = p->q_heads / p->kv_heads;
-  a.rows_per_tile = kQrows / a.group;
+  a.rows_per_tile = prefill_qrows(p->head_dim) / a.group;
   a.tiles = (p->max_rows + a.rows_per_tile - 1) / a.rows_per_tile;
   a.seqs = p->seqs;
   const bool softcap = p->softcap > 0.f;
@@ -1376,7 +1392,8 @@ int paged_prefill(const gk_prefill_params* p, hipStream_t stream) {
   if (items > (int64_t)1 << 30) return fail(GK_ERR_INVALID_ARGUMENT, "gk_paged_prefill: too many rows");
   const dim3 grid((unsigned)items);
   if (p->head_dim == 64) launch<64>(a, softcap, p->block_size, grid, stream);
-  else launch<128>(a, softcap, p->block_size, grid, stream);
+  else if (p->head_dim == 128) launch<128>(a, softcap, p->block_size, grid, stream);
+  else launch<256>(a, softcap, p->block_size, grid, stream);
   return hip_status(hipGetLastError(), "gk_paged_prefill launch");
 }
 

@@ -749,7 +749,7 @@ class PagedMetadata : public torch::CustomClassHolder {
     // supports the geometry; every other row is a decode row. The requests of
     // device-built metadata are filled in on the device below.
     // The prefill kernel takes any page size, the token-granular map included.
-    const bool prefill_ok = (head_dim == 64 || head_dim == 128) && query_heads / kv_heads <= 128;
+    const bool prefill_ok = query_heads / kv_heads <= 128;
     std::vector<int32_t> dec_request, dec_context, dec_map, seq_request, seq_first, seq_rows, seq_prefix;
     for (const auto& run : sequences_) {
       if (prefill_ok && run.length >= kPrefillMinRows) {

@@ -144,7 +144,7 @@ int gk_paged_decode_scratch(const gk_decode_params* params, hipStream_t stream);
  * [left, seq_prefix[s] + i] of block-table row seq_request[s] (causal; left =
  * position - sliding_window + 1 when a window is set, else 0). Every key,
  * including the chunk's own, must already be in the pool (store first).
- * head_dim 64 or 128; GQA group at most 128; block_size any power of two up
+ * head_dim 64, 128 or 256; GQA group at most 128; block_size any power of two up
  * to 2^20, 1 (the token-granular slot map as the block table) included.
  * query, pool and out are 16-byte aligned and the row strides multiples of 8
  * elements (GK_ERR_INVALID_ARGUMENT otherwise).

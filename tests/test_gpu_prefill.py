@@ -92,6 +92,27 @@ def test_prefill_small_blocks_window_evicted(runner, block_size):
     check(reference, runner.run_prefill_case(case), fp32_softmax=True)
 
 
+@pytest.mark.parametrize("geometry", [(16, 8, 256), (8, 1, 256), (6, 6, 256), (24, 2, 256), (128, 1, 256)])
+@pytest.mark.parametrize("block_size", [1, 4, 16, 64])
+def test_prefill_head_dim_256(runner, geometry, block_size):
+    # head_dim 256 (the reference accepts 64, 128 and 256:
+    # src/bridge/attention_plan.cpp:169): one 16-row query tile per wave,
+    # 32-key steps, GQA groups 1-128 (group 128: one chunk row per workgroup).
+    heads, kv_heads, d = geometry
+    case = cases.PrefillCase(700 + heads + block_size, heads, kv_heads, d, block_size, prefixes=[0, 37, 300, 64],
+                             chunks=[1, 45, 130, 77])
+    print("geometry", geometry, "block", block_size, check(case, runner.run_prefill_case(case)), flush=True)
+
+
+@pytest.mark.parametrize("variant", ["window", "softcap", "both"])
+def test_prefill_head_dim_256_window_softcap(runner, variant):
+    # Gemma-2-style attention: head_dim 256, logit softcap and sliding window.
+    case = cases.PrefillCase(31, 16, 8, 256, 16, prefixes=[100, 0, 333], chunks=[90, 200, 17],
+                             softcap=50.0 if variant != "window" else 0.0,
+                             window=70 if variant != "softcap" else -1)
+    check(case, runner.run_prefill_case(case), fp32_softmax=True)
+
+
 def test_prefill_shared_prefix_small(runner):
     case = cases.PrefillCase(4, 32, 8, 128, 128, prefixes=[256] * 4, chunks=[64, 65, 1, 100],
                              shared_prefix_blocks=2)
