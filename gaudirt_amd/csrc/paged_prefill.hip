@@ -383,12 +383,12 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
   };
   // O[qrow][dim] += P . V with pa and the V tile vt, and the row sums. The
   // first half's operands come from vfirst when the caller read them earlier.
-  auto accumulate = [&](const char* vt, const bf16x8_t* vfirst) __attribute__((always_inline)) {
+  auto accumulate = [&](const char* vt, const bf16x8_t* vfirst, int nfirst = S::NO) __attribute__((always_inline)) {
 #pragma unroll
     for (int c = 0; c < S::NO; ++c) {
 #pragma unroll
       for (int hh = 0; hh < kKH; ++hh) {
-        const bf16x8_t v = (hh == 0 && vfirst) ? vfirst[c] : read_v(vt, hh, c);
+        const bf16x8_t v = (hh == 0 && vfirst && c < nfirst) ? vfirst[c] : read_v(vt, hh, c);
 #pragma unroll
         for (int nt = 0; nt < kNT; ++nt) o[nt][c] = mfma32(pa[hh][nt], v, o[nt][c]);
       }
@@ -802,9 +802,15 @@ __global__ __launch_bounds__(kPrefillWaves * 64, 1) void prefill_kernel(PrefillA
         softmax(tb);
         accumulate(kv[cur][1], vfirst);
       } else {
-        // head_dim 256: the early V reads would take 64 more VGPRs.
+        // head_dim 256: half the V operands are read early (32 VGPRs; C4's
+        // shapes at head_dim 256, same box: none 162.7-164.2 us, a quarter
+        // 160.5-162.8, half 158.2-158.7, all 164.9-166.0).
+        constexpr int NF = S::NO / 2;
+        bf16x8_t vfirst[NF];
+#pragma unroll
+        for (int c = 0; c < NF; ++c) vfirst[c] = read_v(kv[cur][1], 0, c);
         softmax(tb);
-        accumulate(kv[cur][1], nullptr);
+        accumulate(kv[cur][1], vfirst, NF);
       }
     };
     int step = 0;
