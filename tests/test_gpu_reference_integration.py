@@ -3,7 +3,8 @@
 - tests/paged_fused_integration_smoke.py: one decode row at prefix 143 and a
   137-row causal prefill from position 0, int32 metadata, the request map
   arange(context) % (slots - 1) + 1, over the geometries its environment
-  selects (4/2, 56/8 heads at head_dim 128; 4/2 at 64);
+  selects (4/2, 56/8 heads at head_dim 128; 4/2 at 64), and 16/8 heads at
+  head_dim 256;
 - tests/paged_tiled_integration_smoke.py: 7- and 137-row chunks on a 512-token
   prefix with the new keys as an unaligned column view, for 1 and 256 requests
   sharing the map;
@@ -83,7 +84,10 @@ def run(torch, heads, kv_heads, dim, slots, mapping, requests, positions, seed, 
     return max_abs, mean_abs, errors
 
 
-@pytest.mark.parametrize("heads,kv_heads,dim", [(4, 2, 128), (56, 8, 128), (4, 2, 64)])
+# The smoke's geometries, plus head_dim 256 (16 q / 8 kv heads), which the
+# reference also accepts and whose 137-row chunk runs the head_dim 256 MFMA
+# prefill through the op.
+@pytest.mark.parametrize("heads,kv_heads,dim", [(4, 2, 128), (56, 8, 128), (4, 2, 64), (16, 8, 256)])
 @pytest.mark.parametrize("case,rows,prefix", [("decode", 1, 143), ("prefill", 137, 0)])
 def test_fused_integration(torch_ext, heads, kv_heads, dim, case, rows, prefix):
     torch = torch_ext
